@@ -1,0 +1,643 @@
+// gdnr_abi.cpp -- the extern "C" boundary of libgdnreplay.so (include/gdnr.h).
+//
+// Each entry point validates shapes, dtypes, strides and alignment on the
+// host, fills a kernel argument block and enqueues the kernels on the
+// caller's stream. Nothing here allocates device memory or synchronises.
+// The reference wrappers validate nothing (prototype/gdn_replayssm_fp8_kernel.py
+// :344-405, :710-795, :1129-1235); misuse there corrupts memory silently,
+// here it is an error code plus a message.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <initializer_list>
+#include <string>
+
+#include "gdnr.h"
+#include "gdnr_internal.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+#define GDNR_TRY(expr)          \
+  do {                          \
+    const int rc_ = (expr);     \
+    if (rc_ != GDNR_OK) return rc_; \
+  } while (0)
+
+int elem_size(int dt) {
+  switch (dt) {
+    case GDNR_DTYPE_BF16:
+    case GDNR_DTYPE_F16: return 2;
+    case GDNR_DTYPE_F32:
+    case GDNR_DTYPE_I32: return 4;
+    case GDNR_DTYPE_I64: return 8;
+    case GDNR_DTYPE_FP8E4M3FN:
+    case GDNR_DTYPE_U8:
+    case GDNR_DTYPE_BOOL: return 1;
+    default: return 0;
+  }
+}
+
+const char* dtype_name(int dt) {
+  switch (dt) {
+    case GDNR_DTYPE_BF16: return "bf16";
+    case GDNR_DTYPE_F16: return "f16";
+    case GDNR_DTYPE_F32: return "f32";
+    case GDNR_DTYPE_FP8E4M3FN: return "fp8e4m3fn";
+    case GDNR_DTYPE_U8: return "u8";
+    case GDNR_DTYPE_I32: return "i32";
+    case GDNR_DTYPE_I64: return "i64";
+    case GDNR_DTYPE_BOOL: return "bool";
+    default: return "?";
+  }
+}
+
+int check_desc(const gdnr_tensor* t, const char* name, int ndim) {
+  if (!t) return fail(GDNR_ERR_INVALID_ARGUMENT, "%s: null tensor descriptor", name);
+  if (t->ndim != ndim) return fail(GDNR_ERR_INVALID_ARGUMENT, "%s: expected %d dims, got %d", name, ndim, t->ndim);
+  if (elem_size(t->dtype) == 0) return fail(GDNR_ERR_INVALID_ARGUMENT, "%s: unknown dtype code %d", name, t->dtype);
+  int64_t numel = 1;
+  for (int d = 0; d < ndim; ++d) {
+    if (t->shape[d] < 0) return fail(GDNR_ERR_INVALID_ARGUMENT, "%s: negative extent in dim %d", name, d);
+    if (t->strides[d] < 0) return fail(GDNR_ERR_INVALID_ARGUMENT, "%s: negative stride in dim %d", name, d);
+    numel *= t->shape[d];
+  }
+  if (numel > 0 && t->data == nullptr) return fail(GDNR_ERR_INVALID_ARGUMENT, "%s: null data pointer", name);
+  return GDNR_OK;
+}
+
+int check_dtype(const gdnr_tensor* t, const char* name, std::initializer_list<int> allowed) {
+  for (int d : allowed)
+    if (t->dtype == d) return GDNR_OK;
+  std::string list;
+  for (int d : allowed) {
+    if (!list.empty()) list += "|";
+    list += dtype_name(d);
+  }
+  return fail(GDNR_ERR_INVALID_ARGUMENT, "%s: dtype %s not accepted (expected %s)", name, dtype_name(t->dtype),
+              list.c_str());
+}
+
+int check_shape(const gdnr_tensor* t, const char* name, std::initializer_list<int64_t> shape) {
+  int d = 0;
+  for (int64_t s : shape) {
+    if (t->shape[d] != s)
+      return fail(GDNR_ERR_INVALID_ARGUMENT, "%s: dim %d is %lld, expected %lld", name, d, (long long)t->shape[d],
+                  (long long)s);
+    ++d;
+  }
+  return GDNR_OK;
+}
+
+int check_inner_unit(const gdnr_tensor* t, const char* name) {
+  const int last = t->ndim - 1;
+  if (t->shape[last] > 1 && t->strides[last] != 1)
+    return fail(GDNR_ERR_INVALID_ARGUMENT, "%s: innermost stride must be 1 (got %lld)", name,
+                (long long)t->strides[last]);
+  return GDNR_OK;
+}
+
+// base pointer and every outer stride (in bytes) must be multiples of `align`
+int check_align(const gdnr_tensor* t, const char* name, int align) {
+  const int es = elem_size(t->dtype);
+  if (((uintptr_t)t->data) % align)
+    return fail(GDNR_ERR_INVALID_ARGUMENT, "%s: data pointer must be %d-byte aligned", name, align);
+  for (int d = 0; d + 1 < t->ndim; ++d)
+    if (t->shape[d] > 1 && (t->strides[d] * es) % align)
+      return fail(GDNR_ERR_INVALID_ARGUMENT, "%s: stride of dim %d (%lld bytes) must be a multiple of %d", name, d,
+                  (long long)(t->strides[d] * es), align);
+  return GDNR_OK;
+}
+
+bool is_act(int dt) { return dt == GDNR_DTYPE_BF16 || dt == GDNR_DTYPE_F16 || dt == GDNR_DTYPE_F32; }
+
+int check_scalar_vec(const gdnr_tensor* t, const char* name, int ndim, std::initializer_list<int64_t> shape) {
+  GDNR_TRY(check_desc(t, name, ndim));
+  GDNR_TRY(check_dtype(t, name, {GDNR_DTYPE_BF16, GDNR_DTYPE_F16, GDNR_DTYPE_F32}));
+  return check_shape(t, name, shape);
+}
+
+// valid_len / pos: int32; flush: one byte (bool | u8) per sequence
+int check_index_vec(const gdnr_tensor* t, const char* name, int64_t batch, bool is_flag) {
+  GDNR_TRY(check_desc(t, name, 1));
+  if (is_flag)
+    GDNR_TRY(check_dtype(t, name, {GDNR_DTYPE_BOOL, GDNR_DTYPE_U8}));
+  else
+    GDNR_TRY(check_dtype(t, name, {GDNR_DTYPE_I32}));
+  return check_shape(t, name, {batch});
+}
+
+struct Geometry {
+  int64_t B, L, H, K, HV, V;
+  int act;
+};
+
+// q [B,H,K] (optional), k_cache [B,L,H,K], v_cache [B,L,HV,V], g/beta [B,L,HV]
+int check_ring(const gdnr_tensor* k_cache, const gdnr_tensor* v_cache, const gdnr_tensor* g_cache,
+               const gdnr_tensor* beta_cache, Geometry* geo, int ring_align) {
+  GDNR_TRY(check_desc(k_cache, "k_cache", 4));
+  GDNR_TRY(check_desc(v_cache, "v_cache", 4));
+  if (!is_act(k_cache->dtype))
+    return fail(GDNR_ERR_INVALID_ARGUMENT, "k_cache: dtype %s not accepted (expected bf16|f16|f32)",
+                dtype_name(k_cache->dtype));
+  geo->act = k_cache->dtype;
+  geo->B = k_cache->shape[0];
+  geo->L = k_cache->shape[1];
+  geo->H = k_cache->shape[2];
+  geo->K = k_cache->shape[3];
+  geo->HV = v_cache->shape[2];
+  geo->V = v_cache->shape[3];
+  if (v_cache->dtype != geo->act)
+    return fail(GDNR_ERR_INVALID_ARGUMENT, "v_cache: dtype %s differs from k_cache's %s", dtype_name(v_cache->dtype),
+                dtype_name(geo->act));
+  GDNR_TRY(check_shape(v_cache, "v_cache", {geo->B, geo->L}));
+  GDNR_TRY(check_scalar_vec(g_cache, "g_cache", 3, {geo->B, geo->L, geo->HV}));
+  GDNR_TRY(check_scalar_vec(beta_cache, "beta_cache", 3, {geo->B, geo->L, geo->HV}));
+  if (g_cache->dtype != geo->act || beta_cache->dtype != geo->act)
+    return fail(GDNR_ERR_UNSUPPORTED, "g_cache/beta_cache dtypes (%s/%s) must equal the k/v ring dtype %s",
+                dtype_name(g_cache->dtype), dtype_name(beta_cache->dtype), dtype_name(geo->act));
+  GDNR_TRY(check_inner_unit(k_cache, "k_cache"));
+  GDNR_TRY(check_inner_unit(v_cache, "v_cache"));
+  GDNR_TRY(check_align(k_cache, "k_cache", ring_align));
+  GDNR_TRY(check_align(v_cache, "v_cache", ring_align));
+  if (geo->K != gdnr::kKeyDim)
+    return fail(GDNR_ERR_UNSUPPORTED, "key head dim K=%lld: only K=%d is built", (long long)geo->K, gdnr::kKeyDim);
+  if (geo->H <= 0 || geo->HV <= 0 || geo->HV % geo->H)
+    return fail(GDNR_ERR_INVALID_ARGUMENT, "value heads (%lld) must be a positive multiple of key heads (%lld)",
+                (long long)geo->HV, (long long)geo->H);
+  if (geo->V <= 0 || geo->V % gdnr::kVBlock)
+    return fail(GDNR_ERR_INVALID_ARGUMENT, "value head dim V=%lld must be a positive multiple of %d",
+                (long long)geo->V, gdnr::kVBlock);
+  if (geo->L < 1 || geo->L > gdnr::kMaxRing)
+    return fail(GDNR_ERR_UNSUPPORTED, "ring length %lld outside [1, %d]", (long long)geo->L, gdnr::kMaxRing);
+  return GDNR_OK;
+}
+
+int largest_group(int64_t G) {
+  for (int gw = gdnr::kMaxWavesPerWG; gw > 1; --gw)
+    if (G % gw == 0) return gw;
+  return 1;
+}
+
+int32_t align16(int64_t x) { return (int32_t)((x + 15) / 16 * 16); }
+
+// LDS layout of the replay workgroup; returns total bytes.
+int32_t layout_lds(gdnr::ReplayArgs* a, int es, bool stage_k, bool stage_v) {
+  const int64_t K = gdnr::kKeyDim;
+  int64_t off = 0;
+  a->lds_q = 0;
+  off = align16(K * es);
+  a->lds_k = (int32_t)off;
+  if (stage_k) off = align16(off + (int64_t)a->L * K * es);
+  a->lds_v = (int32_t)off;
+  if (stage_v) off = align16(off + (int64_t)a->L * a->gw * a->block_v * es);
+  a->lds_gb = (int32_t)off;
+  off = align16(off + (int64_t)a->L * a->gw * 8);
+  a->lds_t = (int32_t)off;
+  off = align16(off + (int64_t)a->gw * K * 4);
+  a->lds_bytes = (int32_t)off;
+  return a->lds_bytes;
+}
+
+constexpr int32_t kMaxLds = 64 * 1024;
+
+// pick the value heads per workgroup so the LDS layout fits
+int fit_lds(gdnr::ReplayArgs* a, int es, bool stage_k, bool stage_v) {
+  for (int gw = largest_group(a->G); gw >= 1; --gw) {
+    if (a->G % gw) continue;
+    a->gw = gw;
+    if (layout_lds(a, es, stage_k, stage_v) <= kMaxLds) return GDNR_OK;
+  }
+  return fail(GDNR_ERR_UNSUPPORTED, "ring length %d with block_v=%d needs %d bytes of LDS (> %d); use a smaller block_v",
+              a->L, a->block_v, a->lds_bytes, kMaxLds);
+}
+
+int check_checkpoint(const gdnr_tensor* checkpoint, const gdnr_tensor* scale, const Geometry& g) {
+  GDNR_TRY(check_desc(checkpoint, "checkpoint", 4));
+  GDNR_TRY(check_dtype(checkpoint, "checkpoint", {GDNR_DTYPE_FP8E4M3FN, GDNR_DTYPE_U8}));
+  GDNR_TRY(check_shape(checkpoint, "checkpoint", {g.B, g.HV, g.V, g.K}));
+  GDNR_TRY(check_inner_unit(checkpoint, "checkpoint"));
+  GDNR_TRY(check_align(checkpoint, "checkpoint", 16));
+  GDNR_TRY(check_desc(scale, "checkpoint_scale", 3));
+  GDNR_TRY(check_dtype(scale, "checkpoint_scale", {GDNR_DTYPE_F16}));
+  return check_shape(scale, "checkpoint_scale", {g.B, g.HV, g.V / gdnr::kVBlock});
+}
+
+int check_act_tensor(const gdnr_tensor* t, const char* name, int ndim, std::initializer_list<int64_t> shape, int act,
+                     int align) {
+  GDNR_TRY(check_desc(t, name, ndim));
+  if (t->dtype != act)
+    return fail(GDNR_ERR_INVALID_ARGUMENT, "%s: dtype %s differs from the ring dtype %s", name, dtype_name(t->dtype),
+                dtype_name(act));
+  GDNR_TRY(check_shape(t, name, shape));
+  GDNR_TRY(check_inner_unit(t, name));
+  return check_align(t, name, align);
+}
+
+int check_block_v(int32_t block_v, const Geometry& g) {
+  if (block_v != 32 && block_v != 64 && block_v != 128)
+    return fail(GDNR_ERR_INVALID_ARGUMENT, "block_v=%d: expected 32, 64 or 128", block_v);
+  if (g.V % block_v) return fail(GDNR_ERR_INVALID_ARGUMENT, "block_v=%d does not divide V=%lld", block_v, (long long)g.V);
+  return GDNR_OK;
+}
+
+void fill_common(gdnr::ReplayArgs* a, const Geometry& g, int32_t block_v) {
+  a->B = (int32_t)g.B;
+  a->H = (int32_t)g.H;
+  a->HV = (int32_t)g.HV;
+  a->G = (int32_t)(g.HV / g.H);
+  a->V = (int32_t)g.V;
+  a->L = (int32_t)g.L;
+  a->block_v = block_v;
+  a->n_vt = (int32_t)(g.V / block_v);
+  a->out_scale = 1.0f / __builtin_sqrtf((float)g.K);
+}
+
+void fill_ckpt(gdnr::ReplayArgs* a, const gdnr_tensor* c, const gdnr_tensor* s) {
+  a->ckpt = (uint8_t*)c->data;
+  a->ck_b = c->strides[0];
+  a->ck_h = c->strides[1];
+  a->ck_v = c->strides[2];
+  a->scale = (uint16_t*)s->data;
+  a->sc_b = s->strides[0];
+  a->sc_h = s->strides[1];
+  a->sc_v = s->strides[2];
+}
+
+void fill_ring(gdnr::ReplayArgs* a, const gdnr_tensor* k, const gdnr_tensor* v, const gdnr_tensor* g,
+               const gdnr_tensor* be) {
+  a->k = k->data;
+  a->k_b = k->strides[0];
+  a->k_t = k->strides[1];
+  a->k_h = k->strides[2];
+  a->v = v->data;
+  a->v_b = v->strides[0];
+  a->v_t = v->strides[1];
+  a->v_h = v->strides[2];
+  a->g = g->data;
+  a->g_b = g->strides[0];
+  a->g_t = g->strides[1];
+  a->g_h = g->strides[2];
+  a->beta = be->data;
+  a->be_b = be->strides[0];
+  a->be_t = be->strides[1];
+  a->be_h = be->strides[2];
+}
+
+template <class T>
+void fill_index(const gdnr_tensor* t, const T** p, int64_t* s) {
+  *p = (const T*)t->data;
+  *s = t->strides[0];
+}
+
+int launch_replay(const gdnr::ReplayArgs& a, int act, int mode, bool gate_f32, void* stream) {
+  if (act == GDNR_DTYPE_BF16) return gdnr::launch_replay_bf16(a, mode, gate_f32, stream);
+  if (act == GDNR_DTYPE_F16) return gdnr::launch_replay_f16(a, mode, gate_f32, stream);
+  return gdnr::launch_replay_f32(a, mode, gate_f32, stream);
+}
+int launch_precompute(const gdnr::ReplayArgs& a, int act, void* stream) {
+  if (act == GDNR_DTYPE_BF16) return gdnr::launch_precompute_bf16(a, stream);
+  if (act == GDNR_DTYPE_F16) return gdnr::launch_precompute_f16(a, stream);
+  return gdnr::launch_precompute_f32(a, stream);
+}
+int launch_prep(const gdnr::PrepArgs& a, int act, bool gate_f32, void* stream) {
+  if (act == GDNR_DTYPE_BF16) return gdnr::launch_prep_bf16(a, gate_f32, stream);
+  if (act == GDNR_DTYPE_F16) return gdnr::launch_prep_f16(a, gate_f32, stream);
+  return gdnr::launch_prep_f32(a, gate_f32, stream);
+}
+
+int hip_status(int rc) {
+  if (rc == 0) return GDNR_OK;
+  return fail(GDNR_ERR_HIP, "kernel launch failed: %s", gdnr::hip_error_string(rc));
+}
+
+int check_prep_inputs(const gdnr_tensor* mixed_qkv, const gdnr_tensor* a, const gdnr_tensor* b,
+                      const gdnr_tensor* a_log, const gdnr_tensor* dt_bias, const gdnr_tensor* pos, const Geometry& g) {
+  GDNR_TRY(check_desc(mixed_qkv, "mixed_qkv", 2));
+  if (mixed_qkv->dtype != g.act)
+    return fail(GDNR_ERR_INVALID_ARGUMENT, "mixed_qkv: dtype %s differs from the ring dtype %s",
+                dtype_name(mixed_qkv->dtype), dtype_name(g.act));
+  const int64_t width = 2 * g.H * g.K + g.HV * g.V;
+  if (mixed_qkv->shape[0] != g.B || mixed_qkv->shape[1] < width)
+    return fail(GDNR_ERR_INVALID_ARGUMENT, "mixed_qkv: shape [%lld, %lld], expected [%lld, >= %lld]",
+                (long long)mixed_qkv->shape[0], (long long)mixed_qkv->shape[1], (long long)g.B, (long long)width);
+  GDNR_TRY(check_inner_unit(mixed_qkv, "mixed_qkv"));
+  GDNR_TRY(check_align(mixed_qkv, "mixed_qkv", 4));
+  GDNR_TRY(check_scalar_vec(a, "a", 2, {g.B, g.HV}));
+  GDNR_TRY(check_scalar_vec(b, "b", 2, {g.B, g.HV}));
+  if (a->dtype != b->dtype || (a->dtype != g.act && a->dtype != GDNR_DTYPE_F32))
+    return fail(GDNR_ERR_UNSUPPORTED, "a/b dtypes (%s/%s) must match each other and be f32 or the ring dtype %s",
+                dtype_name(a->dtype), dtype_name(b->dtype), dtype_name(g.act));
+  GDNR_TRY(check_desc(a_log, "a_log", 1));
+  GDNR_TRY(check_dtype(a_log, "a_log", {GDNR_DTYPE_F32}));
+  GDNR_TRY(check_shape(a_log, "a_log", {g.HV}));
+  GDNR_TRY(check_desc(dt_bias, "dt_bias", 1));
+  GDNR_TRY(check_dtype(dt_bias, "dt_bias", {GDNR_DTYPE_F32}));
+  GDNR_TRY(check_shape(dt_bias, "dt_bias", {g.HV}));
+  return check_index_vec(pos, "pos", g.B, false);
+}
+
+void fill_prep_inputs(gdnr::ReplayArgs* r, const gdnr_tensor* mixed_qkv, const gdnr_tensor* a, const gdnr_tensor* b,
+                      const gdnr_tensor* a_log, const gdnr_tensor* dt_bias, const gdnr_tensor* pos,
+                      const gdnr_tensor* q_out) {
+  r->mixed = mixed_qkv->data;
+  r->mx_b = mixed_qkv->strides[0];
+  r->a = a->data;
+  r->a_b = a->strides[0];
+  r->a_h = a->strides[1];
+  r->bgate = b->data;
+  r->bg_b = b->strides[0];
+  r->bg_h = b->strides[1];
+  r->a_log = (const float*)a_log->data;
+  r->al_s = a_log->strides[0];
+  r->dt_bias = (const float*)dt_bias->data;
+  r->db_s = dt_bias->strides[0];
+  fill_index(pos, &r->pos, &r->pos_s);
+  r->q_out = q_out->data;
+  r->qo_b = q_out->strides[0];
+  r->qo_h = q_out->strides[1];
+}
+
+int check_quant(const gdnr_tensor* state, const gdnr_tensor* payload, const gdnr_tensor* scale, int64_t* B,
+                int64_t* HV, int64_t* V) {
+  GDNR_TRY(check_desc(state, "state", 4));
+  GDNR_TRY(check_dtype(state, "state", {GDNR_DTYPE_F32}));
+  *B = state->shape[0];
+  *HV = state->shape[1];
+  *V = state->shape[2];
+  if (state->shape[3] != gdnr::kKeyDim)
+    return fail(GDNR_ERR_UNSUPPORTED, "key head dim K=%lld: only K=%d is built", (long long)state->shape[3],
+                gdnr::kKeyDim);
+  if (*V % gdnr::kVBlock)
+    return fail(GDNR_ERR_INVALID_ARGUMENT, "value head dim V=%lld must be a multiple of %d", (long long)*V,
+                gdnr::kVBlock);
+  GDNR_TRY(check_inner_unit(state, "state"));
+  GDNR_TRY(check_align(state, "state", 16));
+  GDNR_TRY(check_desc(payload, "payload", 4));
+  GDNR_TRY(check_dtype(payload, "payload", {GDNR_DTYPE_FP8E4M3FN, GDNR_DTYPE_U8}));
+  GDNR_TRY(check_shape(payload, "payload", {*B, *HV, *V, (int64_t)gdnr::kKeyDim}));
+  GDNR_TRY(check_inner_unit(payload, "payload"));
+  GDNR_TRY(check_align(payload, "payload", 16));
+  GDNR_TRY(check_desc(scale, "scale", 3));
+  GDNR_TRY(check_dtype(scale, "scale", {GDNR_DTYPE_F16, GDNR_DTYPE_F32}));
+  return check_shape(scale, "scale", {*B, *HV, *V / gdnr::kVBlock});
+}
+
+void fill_quant(gdnr::QuantArgs* q, const gdnr_tensor* state, const gdnr_tensor* payload, const gdnr_tensor* scale,
+                int64_t B, int64_t HV, int64_t V) {
+  q->state = (const float*)state->data;
+  q->st_b = state->strides[0];
+  q->st_h = state->strides[1];
+  q->st_v = state->strides[2];
+  q->codes = (uint8_t*)payload->data;
+  q->ck_b = payload->strides[0];
+  q->ck_h = payload->strides[1];
+  q->ck_v = payload->strides[2];
+  q->scale = scale->data;
+  q->sc_b = scale->strides[0];
+  q->sc_h = scale->strides[1];
+  q->sc_v = scale->strides[2];
+  q->scale_dt = scale->dtype;
+  q->saturated = nullptr;
+  q->B = (int32_t)B;
+  q->HV = (int32_t)HV;
+  q->V = (int32_t)V;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* gdnr_last_error(void) { return g_last_error.c_str(); }
+
+int gdnr_abi_version(void) { return GDNR_ABI_VERSION; }
+
+int gdnr_replay_fp8(const gdnr_tensor* checkpoint, const gdnr_tensor* checkpoint_scale, const gdnr_tensor* q,
+                    const gdnr_tensor* k_cache, const gdnr_tensor* v_cache, const gdnr_tensor* g_cache,
+                    const gdnr_tensor* beta_cache, const gdnr_tensor* valid_len, const gdnr_tensor* flush,
+                    const gdnr_tensor* out, int32_t block_v, void* stream) {
+  g_last_error.clear();
+  Geometry g;
+  GDNR_TRY(check_ring(k_cache, v_cache, g_cache, beta_cache, &g, 16));
+  GDNR_TRY(check_checkpoint(checkpoint, checkpoint_scale, g));
+  GDNR_TRY(check_act_tensor(q, "q", 3, {g.B, g.H, g.K}, g.act, 16));
+  GDNR_TRY(check_index_vec(valid_len, "valid_len", g.B, false));
+  GDNR_TRY(check_index_vec(flush, "flush", g.B, true));
+  GDNR_TRY(check_act_tensor(out, "out", 3, {g.B, g.HV, g.V}, g.act, 2));
+  GDNR_TRY(check_block_v(block_v, g));
+  if (g.B == 0) return GDNR_OK;
+  gdnr::ReplayArgs a = {};
+  fill_common(&a, g, block_v);
+  fill_ckpt(&a, checkpoint, checkpoint_scale);
+  fill_ring(&a, k_cache, v_cache, g_cache, beta_cache);
+  a.q = q->data;
+  a.q_b = q->strides[0];
+  a.q_h = q->strides[1];
+  fill_index(valid_len, &a.valid_len, &a.vl_s);
+  fill_index(flush, &a.flush, &a.fl_s);
+  a.out = out->data;
+  a.o_b = out->strides[0];
+  a.o_h = out->strides[1];
+  GDNR_TRY(fit_lds(&a, elem_size(g.act), true, true));
+  return hip_status(launch_replay(a, g.act, gdnr::kModeReplay, false, stream));
+}
+
+int gdnr_replay_fp8_split(const gdnr_tensor* checkpoint, const gdnr_tensor* checkpoint_scale, const gdnr_tensor* q,
+                          const gdnr_tensor* k_cache, const gdnr_tensor* v_cache, const gdnr_tensor* g_cache,
+                          const gdnr_tensor* beta_cache, const gdnr_tensor* valid_len,
+                          const gdnr_tensor* transformed_query, const gdnr_tensor* coefficient,
+                          const gdnr_tensor* out, int32_t block_v, int32_t block_kc, int32_t precompute_grouped,
+                          void* stream) {
+  g_last_error.clear();
+  Geometry g;
+  GDNR_TRY(check_ring(k_cache, v_cache, g_cache, beta_cache, &g, 16));
+  GDNR_TRY(check_checkpoint(checkpoint, checkpoint_scale, g));
+  GDNR_TRY(check_act_tensor(q, "q", 3, {g.B, g.H, g.K}, g.act, 16));
+  GDNR_TRY(check_index_vec(valid_len, "valid_len", g.B, false));
+  GDNR_TRY(check_desc(transformed_query, "transformed_query_buffer", 3));
+  GDNR_TRY(check_dtype(transformed_query, "transformed_query_buffer", {GDNR_DTYPE_F32}));
+  GDNR_TRY(check_shape(transformed_query, "transformed_query_buffer", {g.B, g.HV, g.K}));
+  GDNR_TRY(check_inner_unit(transformed_query, "transformed_query_buffer"));
+  GDNR_TRY(check_align(transformed_query, "transformed_query_buffer", 16));
+  GDNR_TRY(check_desc(coefficient, "coefficient_buffer", 3));
+  GDNR_TRY(check_dtype(coefficient, "coefficient_buffer", {GDNR_DTYPE_F32}));
+  GDNR_TRY(check_shape(coefficient, "coefficient_buffer", {g.B, g.HV}));
+  if (coefficient->shape[2] < g.L)
+    return fail(GDNR_ERR_INVALID_ARGUMENT, "coefficient_buffer: last dim %lld is shorter than the ring (%lld)",
+                (long long)coefficient->shape[2], (long long)g.L);
+  GDNR_TRY(check_act_tensor(out, "out", 3, {g.B, g.HV, g.V}, g.act, 2));
+  GDNR_TRY(check_block_v(block_v, g));
+  if (block_kc != 128 && block_kc != g.K)
+    return fail(GDNR_ERR_UNSUPPORTED, "block_kc=%d: the checkpoint is streamed in whole 128-column rows", block_kc);
+  if (g.B == 0) return GDNR_OK;
+
+  gdnr::ReplayArgs a = {};
+  fill_common(&a, g, block_v);
+  fill_ckpt(&a, checkpoint, checkpoint_scale);
+  fill_ring(&a, k_cache, v_cache, g_cache, beta_cache);
+  a.q = q->data;
+  a.q_b = q->strides[0];
+  a.q_h = q->strides[1];
+  fill_index(valid_len, &a.valid_len, &a.vl_s);
+  a.flush = nullptr;
+  a.tq = (float*)transformed_query->data;
+  a.tq_b = transformed_query->strides[0];
+  a.tq_h = transformed_query->strides[1];
+  a.coef = (float*)coefficient->data;
+  a.co_b = coefficient->strides[0];
+  a.co_h = coefficient->strides[1];
+  a.co_t = coefficient->strides[2];
+  a.out = out->data;
+  a.o_b = out->strides[0];
+  a.o_h = out->strides[1];
+
+  // precompute: one workgroup per key head (grouped) or per value head
+  gdnr::ReplayArgs pre = a;
+  pre.block_v = 32;
+  pre.n_vt = 1;
+  if (precompute_grouped) {
+    GDNR_TRY(fit_lds(&pre, elem_size(g.act), true, false));
+  } else {
+    pre.gw = 1;
+    layout_lds(&pre, elem_size(g.act), true, false);
+  }
+  GDNR_TRY(hip_status(launch_precompute(pre, g.act, stream)));
+  GDNR_TRY(fit_lds(&a, elem_size(g.act), false, true));
+  return hip_status(launch_replay(a, g.act, gdnr::kModeApply, false, stream));
+}
+
+int gdnr_prep_ring(const gdnr_tensor* mixed_qkv, const gdnr_tensor* a, const gdnr_tensor* b,
+                   const gdnr_tensor* a_log, const gdnr_tensor* dt_bias, const gdnr_tensor* pos,
+                   const gdnr_tensor* q_out, const gdnr_tensor* k_ring, const gdnr_tensor* v_ring,
+                   const gdnr_tensor* g_ring, const gdnr_tensor* beta_ring, int32_t fused, void* stream) {
+  (void)fused;
+  g_last_error.clear();
+  Geometry g;
+  GDNR_TRY(check_ring(k_ring, v_ring, g_ring, beta_ring, &g, 4));
+  GDNR_TRY(check_act_tensor(q_out, "q_out", 3, {g.B, g.H, g.K}, g.act, 4));
+  GDNR_TRY(check_prep_inputs(mixed_qkv, a, b, a_log, dt_bias, pos, g));
+  if (g.B == 0) return GDNR_OK;
+  gdnr::ReplayArgs r = {};
+  fill_prep_inputs(&r, mixed_qkv, a, b, a_log, dt_bias, pos, q_out);
+  gdnr::PrepArgs p = {};
+  p.mixed = r.mixed;
+  p.mx_b = r.mx_b;
+  p.a = r.a;
+  p.a_b = r.a_b;
+  p.a_h = r.a_h;
+  p.bgate = r.bgate;
+  p.bg_b = r.bg_b;
+  p.bg_h = r.bg_h;
+  p.a_log = r.a_log;
+  p.al_s = r.al_s;
+  p.dt_bias = r.dt_bias;
+  p.db_s = r.db_s;
+  p.pos = r.pos;
+  p.pos_s = r.pos_s;
+  p.q_out = r.q_out;
+  p.qo_b = r.qo_b;
+  p.qo_h = r.qo_h;
+  p.k = k_ring->data;
+  p.k_b = k_ring->strides[0];
+  p.k_t = k_ring->strides[1];
+  p.k_h = k_ring->strides[2];
+  p.v = v_ring->data;
+  p.v_b = v_ring->strides[0];
+  p.v_t = v_ring->strides[1];
+  p.v_h = v_ring->strides[2];
+  p.g = g_ring->data;
+  p.g_b = g_ring->strides[0];
+  p.g_t = g_ring->strides[1];
+  p.g_h = g_ring->strides[2];
+  p.beta = beta_ring->data;
+  p.be_b = beta_ring->strides[0];
+  p.be_t = beta_ring->strides[1];
+  p.be_h = beta_ring->strides[2];
+  p.B = (int32_t)g.B;
+  p.H = (int32_t)g.H;
+  p.HV = (int32_t)g.HV;
+  p.G = (int32_t)(g.HV / g.H);
+  p.V = (int32_t)g.V;
+  p.L = (int32_t)g.L;
+  return hip_status(launch_prep(p, g.act, a->dtype == GDNR_DTYPE_F32, stream));
+}
+
+int gdnr_prep_replay_fp8(const gdnr_tensor* mixed_qkv, const gdnr_tensor* a, const gdnr_tensor* b,
+                         const gdnr_tensor* a_log, const gdnr_tensor* dt_bias, const gdnr_tensor* pos,
+                         const gdnr_tensor* checkpoint, const gdnr_tensor* checkpoint_scale,
+                         const gdnr_tensor* q_out, const gdnr_tensor* k_ring, const gdnr_tensor* v_ring,
+                         const gdnr_tensor* g_ring, const gdnr_tensor* beta_ring, const gdnr_tensor* valid_len,
+                         const gdnr_tensor* flush, const gdnr_tensor* out, int32_t block_v, void* stream) {
+  g_last_error.clear();
+  Geometry g;
+  GDNR_TRY(check_ring(k_ring, v_ring, g_ring, beta_ring, &g, 16));
+  GDNR_TRY(check_checkpoint(checkpoint, checkpoint_scale, g));
+  GDNR_TRY(check_act_tensor(q_out, "q_out", 3, {g.B, g.H, g.K}, g.act, 4));
+  GDNR_TRY(check_prep_inputs(mixed_qkv, a, b, a_log, dt_bias, pos, g));
+  GDNR_TRY(check_index_vec(valid_len, "valid_len", g.B, false));
+  GDNR_TRY(check_index_vec(flush, "flush", g.B, true));
+  GDNR_TRY(check_act_tensor(out, "out", 3, {g.B, g.HV, g.V}, g.act, 2));
+  GDNR_TRY(check_block_v(block_v, g));
+  if (g.B == 0) return GDNR_OK;
+  gdnr::ReplayArgs r = {};
+  fill_common(&r, g, block_v);
+  fill_ckpt(&r, checkpoint, checkpoint_scale);
+  fill_ring(&r, k_ring, v_ring, g_ring, beta_ring);
+  fill_prep_inputs(&r, mixed_qkv, a, b, a_log, dt_bias, pos, q_out);
+  r.q = q_out->data;
+  r.q_b = q_out->strides[0];
+  r.q_h = q_out->strides[1];
+  fill_index(valid_len, &r.valid_len, &r.vl_s);
+  fill_index(flush, &r.flush, &r.fl_s);
+  r.out = out->data;
+  r.o_b = out->strides[0];
+  r.o_h = out->strides[1];
+  GDNR_TRY(fit_lds(&r, elem_size(g.act), true, true));
+  return hip_status(launch_replay(r, g.act, gdnr::kModeFused, a->dtype == GDNR_DTYPE_F32, stream));
+}
+
+int gdnr_quantize_vblock32(const gdnr_tensor* state, const gdnr_tensor* payload, const gdnr_tensor* scale,
+                           const gdnr_tensor* saturated, void* stream) {
+  g_last_error.clear();
+  int64_t B, HV, V;
+  GDNR_TRY(check_quant(state, payload, scale, &B, &HV, &V));
+  if (saturated) {
+    GDNR_TRY(check_desc(saturated, "saturated", 3));
+    GDNR_TRY(check_dtype(saturated, "saturated", {GDNR_DTYPE_I32}));
+    GDNR_TRY(check_shape(saturated, "saturated", {B, HV, V / gdnr::kVBlock}));
+  }
+  if (B * HV * V == 0) return GDNR_OK;
+  gdnr::QuantArgs q = {};
+  fill_quant(&q, state, payload, scale, B, HV, V);
+  if (saturated) {
+    q.saturated = (int32_t*)saturated->data;
+    q.sa_b = saturated->strides[0];
+    q.sa_h = saturated->strides[1];
+    q.sa_v = saturated->strides[2];
+  }
+  return hip_status(gdnr::launch_quantize(q, stream));
+}
+
+int gdnr_dequantize_vblock32(const gdnr_tensor* payload, const gdnr_tensor* scale, const gdnr_tensor* state,
+                             void* stream) {
+  g_last_error.clear();
+  int64_t B, HV, V;
+  GDNR_TRY(check_quant(state, payload, scale, &B, &HV, &V));
+  if (B * HV * V == 0) return GDNR_OK;
+  gdnr::QuantArgs q = {};
+  fill_quant(&q, state, payload, scale, B, HV, V);
+  return hip_status(gdnr::launch_dequantize(q, stream));
+}
+
+}  // extern "C"

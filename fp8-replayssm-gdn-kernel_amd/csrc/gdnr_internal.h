@@ -1,0 +1,97 @@
+// gdnr_internal.h -- kernel argument blocks shared by the C-ABI layer
+// (gdnr_abi.cpp, host validation) and the HIP kernels (gdnr_kernels.hip).
+// All strides are in elements of the tensor they index.
+#pragma once
+
+#include <stdint.h>
+
+namespace gdnr {
+
+enum DType : int32_t {
+  DT_BF16 = 0, DT_F16 = 1, DT_F32 = 2, DT_FP8 = 3, DT_U8 = 4, DT_I32 = 5, DT_I64 = 6, DT_BOOL = 7
+};
+
+constexpr int kKeyDim = 128;      // K: the only head_k_dim built (Qwen3.5 / Qwen3-Next GDN)
+constexpr int kVBlock = 32;       // V-rows per checkpoint scale
+constexpr int kMaxRing = 64;      // ring capacity bound (one VGPR lane per token)
+constexpr int kMaxWavesPerWG = 4; // value heads per workgroup (one wave each)
+
+// Replay / flush / split-apply / fused prep+replay: one workgroup per
+// (sequence b, group of gw value heads sharing key head h, V-tile vt).
+//
+// Hot-path dtypes are compile-time: q, k/v/g/beta rings, out and mixed_qkv
+// share the activation dtype (template), the checkpoint scale is fp16,
+// valid_len/pos are int32, flush is one byte per sequence, a/b are the
+// activation dtype or f32 (template), A_log/dt_bias are f32.
+struct ReplayArgs {
+  uint8_t* ckpt; int64_t ck_b, ck_h, ck_v;
+  uint16_t* scale; int64_t sc_b, sc_h, sc_v;      // fp16 bits
+  const void* q; int64_t q_b, q_h;
+  void* k; int64_t k_b, k_t, k_h;
+  void* v; int64_t v_b, v_t, v_h;
+  void* g; int64_t g_b, g_t, g_h;
+  void* beta; int64_t be_b, be_t, be_h;
+  const int32_t* valid_len; int64_t vl_s;
+  const uint8_t* flush; int64_t fl_s;              // nullptr: never flush
+  void* out; int64_t o_b, o_h;
+  // split buffers: precompute writes them, apply reads them
+  float* tq; int64_t tq_b, tq_h;
+  float* coef; int64_t co_b, co_h, co_t;
+  // fused preparation (prep_replay)
+  const void* mixed; int64_t mx_b;
+  const void* a; int64_t a_b, a_h;
+  const void* bgate; int64_t bg_b, bg_h;
+  const float* a_log; int64_t al_s;
+  const float* dt_bias; int64_t db_s;
+  const int32_t* pos; int64_t pos_s;
+  void* q_out; int64_t qo_b, qo_h;
+  // geometry
+  int32_t B, H, HV, G, V, L;   // L = ring capacity (tensor dim 1)
+  int32_t gw;                  // value heads (waves) per workgroup, divides G
+  int32_t block_v, n_vt;       // V rows per workgroup, V / block_v
+  float out_scale;             // K^-1/2
+  // LDS byte offsets (computed on the host)
+  int32_t lds_q, lds_k, lds_v, lds_gb, lds_t, lds_bytes;
+};
+
+struct PrepArgs {
+  const void* mixed; int64_t mx_b;
+  const void* a; int64_t a_b, a_h;
+  const void* bgate; int64_t bg_b, bg_h;
+  const float* a_log; int64_t al_s;
+  const float* dt_bias; int64_t db_s;
+  const int32_t* pos; int64_t pos_s;
+  void* q_out; int64_t qo_b, qo_h;
+  void* k; int64_t k_b, k_t, k_h;
+  void* v; int64_t v_b, v_t, v_h;
+  void* g; int64_t g_b, g_t, g_h;
+  void* beta; int64_t be_b, be_t, be_h;
+  int32_t B, H, HV, G, V, L;
+};
+
+struct QuantArgs {
+  const float* state; int64_t st_b, st_h, st_v;   // quantise reads, dequantise writes (as float*)
+  uint8_t* codes; int64_t ck_b, ck_h, ck_v;
+  void* scale; int64_t sc_b, sc_h, sc_v; int32_t scale_dt;
+  int32_t* saturated; int64_t sa_b, sa_h, sa_v;   // may be null
+  int32_t B, HV, V;
+};
+
+// Launch modes of the replay kernel.
+enum ReplayMode : int { kModeReplay = 0, kModeApply = 1, kModeFused = 2 };
+
+// Launchers: one set per activation dtype, each in its own translation unit
+// (gdnr_kernels.hip compiled with GDNR_ACT=0/1/2). Return 0 or a hipError_t.
+#define GDNR_DECLARE_LAUNCHERS(SUFFIX)                                                      \
+  int launch_replay_##SUFFIX(const ReplayArgs& a, int mode, bool gate_f32, void* stream); \
+  int launch_precompute_##SUFFIX(const ReplayArgs& a, void* stream);                      \
+  int launch_prep_##SUFFIX(const PrepArgs& a, bool gate_f32, void* stream);
+GDNR_DECLARE_LAUNCHERS(bf16)
+GDNR_DECLARE_LAUNCHERS(f16)
+GDNR_DECLARE_LAUNCHERS(f32)
+#undef GDNR_DECLARE_LAUNCHERS
+int launch_quantize(const QuantArgs& a, void* stream);
+int launch_dequantize(const QuantArgs& a, void* stream);
+const char* hip_error_string(int code);
+
+}  // namespace gdnr

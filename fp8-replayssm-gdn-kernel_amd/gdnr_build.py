@@ -1,0 +1,79 @@
+"""Build libgdnreplay.so (the HIP kernels + the C-ABI layer) for gfx950.
+
+    python gdnr_build.py [-v]
+
+Objects go to _build/ next to this file; the library is written in-tree
+(next to this file) so it travels with the source tree to the GPU host.
+The C-ABI validation layer (csrc/gdnr_abi.cpp) is plain C++ compiled by g++;
+the kernels (csrc/gdnr_kernels.hip) by hipcc. Packed-FP32 VALU instructions
+are disabled for all device code.
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+PKG_DIR = Path(__file__).resolve().parent
+CSRC = PKG_DIR / "csrc"
+INCLUDE = PKG_DIR.parent / "include"
+BUILD_DIR = PKG_DIR / "_build"
+LIBRARY = PKG_DIR / "libgdnreplay.so"
+ARCH = os.environ.get("GDNR_OFFLOAD_ARCH", "gfx950")
+
+HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+DEVICE_FLAGS = [
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall", "-Wno-unused-result",
+]
+HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra"]
+ACTS = ("bf16", "f16", "f32")  # activation dtypes, one kernel object each (GDNR_ACT = index)
+
+
+def _run(cmd: list[str], verbose: bool) -> None:
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    noise = "is not a recognized feature for this target"
+    stderr = "\n".join(line for line in proc.stderr.splitlines() if noise not in line)
+    if proc.returncode != 0:
+        raise RuntimeError(f"build step failed ({proc.returncode}): {' '.join(cmd)}\n{stderr}")
+    if verbose and stderr.strip():
+        print(stderr, file=sys.stderr)
+
+
+def build(verbose: bool = False) -> Path:
+    BUILD_DIR.mkdir(exist_ok=True)
+    inc = [f"-I{INCLUDE}", f"-I{CSRC}"]
+    kern_objs = [BUILD_DIR / f"gdnr_kernels_{act}.o" for act in ACTS]
+    abi_obj = BUILD_DIR / "gdnr_abi.o"
+    jobs = [[HIPCC, *DEVICE_FLAGS, *inc, f"-DGDNR_ACT={i}", "-c", str(CSRC / "gdnr_kernels.hip"), "-o", str(obj)]
+            for i, obj in enumerate(kern_objs)]
+    jobs.append(["g++", *HOST_FLAGS, *inc, "-c", str(CSRC / "gdnr_abi.cpp"), "-o", str(abi_obj)])
+    with ThreadPoolExecutor(max_workers=len(jobs)) as pool:
+        for future in [pool.submit(_run, cmd, verbose) for cmd in jobs]:
+            future.result()
+    tmp = LIBRARY.with_name(LIBRARY.name + ".tmp")
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, kern_objs), str(abi_obj), "-o", str(tmp)],
+         verbose)
+    tmp.replace(LIBRARY)
+    return LIBRARY
+
+
+def device_assembly(act: str = "bf16", out: Path | None = None, verbose: bool = False) -> Path:
+    """Write the gfx950 assembly of one activation dtype's kernels (for the
+    ISA contract tests)."""
+    out = out or BUILD_DIR / f"gdnr_kernels_{act}.s"
+    BUILD_DIR.mkdir(exist_ok=True)
+    _run([HIPCC, *DEVICE_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", f"-DGDNR_ACT={ACTS.index(act)}", "--cuda-device-only",
+          "-S", str(CSRC / "gdnr_kernels.hip"), "-o", str(out)], verbose)
+    return out
+
+
+if __name__ == "__main__":
+    print(build(verbose="-v" in sys.argv))

@@ -1,0 +1,181 @@
+/*
+ * gdnr.h -- C ABI of libgdnreplay.so: the ReplaySSM decode path of gated
+ * delta-rule (GDN) layers, written for AMD Instinct MI355X (gfx950).
+ *
+ * The path keeps each sequence's recurrent state S [HV, V, K] as an
+ * FP8-E4M3FN checkpoint with one fp16 scale per 32 V-rows x K ("vblock32"),
+ * plus a ring of the last L tokens' (k, v, g, beta). A decode step replays
+ * the ring against the dequantised checkpoint and emits o = S q * K^-1/2
+ * without materialising S; when the ring fills, the state is rebuilt and
+ * requantised in place ("flush").
+ *
+ * Conventions shared by every entry point:
+ *  - Tensors are passed as gdnr_tensor: a device pointer, a dtype code,
+ *    the logical shape and per-dimension strides counted in ELEMENTS.
+ *    Outer strides are arbitrary; the innermost (K or V) stride must be 1.
+ *  - `stream` is a hipStream_t (NULL = the default stream). Kernels are
+ *    enqueued asynchronously; no entry point synchronises the device.
+ *  - The library allocates no device memory: every buffer is caller-owned.
+ *  - No C++ exception crosses the ABI. A nonzero return code means nothing
+ *    was launched; gdnr_last_error() (thread-local) says why.
+ *  - Arguments are validated on the host before any HIP call, so a bad
+ *    shape, dtype, stride or alignment is an error, never a silent
+ *    out-of-bounds access. Per-sequence device metadata (valid_len, pos) is
+ *    clamped in the kernels: valid_len to [0, ring length]; a pos outside
+ *    [0, ring length) appends nothing.
+ */
+#ifndef GDNR_H
+#define GDNR_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GDNR_ABI_VERSION 1
+#define GDNR_MAX_DIMS 4
+
+typedef enum gdnr_dtype {
+  GDNR_DTYPE_BF16 = 0,
+  GDNR_DTYPE_F16 = 1,
+  GDNR_DTYPE_F32 = 2,
+  GDNR_DTYPE_FP8E4M3FN = 3, /* OCP e4m3fn: bias 7, max 448, no inf, 0x7F/0xFF NaN */
+  GDNR_DTYPE_U8 = 4,        /* accepted wherever fp8 codes are: raw bytes */
+  GDNR_DTYPE_I32 = 5,
+  GDNR_DTYPE_I64 = 6,
+  GDNR_DTYPE_BOOL = 7
+} gdnr_dtype;
+
+typedef struct gdnr_tensor {
+  void* data;                       /* device pointer */
+  int32_t dtype;                    /* gdnr_dtype */
+  int32_t ndim;                     /* 1..GDNR_MAX_DIMS */
+  int64_t shape[GDNR_MAX_DIMS];
+  int64_t strides[GDNR_MAX_DIMS];   /* in elements */
+} gdnr_tensor;
+
+enum {
+  GDNR_OK = 0,
+  GDNR_ERR_INVALID_ARGUMENT = 1, /* shape / dtype / stride / alignment misuse */
+  GDNR_ERR_UNSUPPORTED = 2,      /* legal for the reference, not built here (e.g. K != 128) */
+  GDNR_ERR_HIP = 3               /* a HIP runtime call failed */
+};
+
+/* Thread-local description of the last failure on this thread ("" if none). */
+const char* gdnr_last_error(void);
+
+/* GDNR_ABI_VERSION of the loaded library. */
+int gdnr_abi_version(void);
+
+/*
+ * One decode step of the replay, per sequence b:
+ *   flush[b] == 0: adjoint replay of ring tokens [0, valid_len[b]) against the
+ *                  dequantised checkpoint; writes out[b] only.
+ *   flush[b] != 0: forward rebuild of the state over the same tokens, writes
+ *                  out[b] from the rebuilt fp32 state, then requantises it to
+ *                  vblock32 IN PLACE (checkpoint[b], checkpoint_scale[b]).
+ * Shapes: checkpoint [B,HV,V,K] fp8/u8; checkpoint_scale [B,HV,V/32] f16|f32;
+ *   q [B,H,K]; k_cache [B,L,H,K]; v_cache [B,L,HV,V]; g_cache, beta_cache
+ *   [B,L,HV]; valid_len [B] i32|i64; flush [B] bool|u8|i32; out [B,HV,V].
+ *   q, k_cache, v_cache and out share one dtype (bf16|f16|f32); g and beta
+ *   may each be bf16|f16|f32. K == 128, V % 32 == 0, HV % H == 0, L <= 64.
+ * block_v (32|64|128, dividing V) is the number of V-rows one workgroup
+ *   streams; unlike the reference it does not constrain the flush.
+ * Replaces gdn_replay_fp8, prototype/gdn_replayssm_fp8_kernel.py:344-405
+ * (device work: _gdn_replay_fp8_kernel, same file :20-242).
+ */
+int gdnr_replay_fp8(const gdnr_tensor* checkpoint, const gdnr_tensor* checkpoint_scale,
+                    const gdnr_tensor* q, const gdnr_tensor* k_cache,
+                    const gdnr_tensor* v_cache, const gdnr_tensor* g_cache,
+                    const gdnr_tensor* beta_cache, const gdnr_tensor* valid_len,
+                    const gdnr_tensor* flush, const gdnr_tensor* out,
+                    int32_t block_v, void* stream);
+
+/*
+ * Non-flush replay as two launches: a precompute that writes the
+ * transformed query T_0 into transformed_query [B,HV,K] f32 and the
+ * per-token coefficients c_t = beta_t (k_t . T_t) into coefficient
+ * [B,HV,Lc] f32 (Lc >= ring length; only t < valid_len[b] is written), then
+ * an apply that streams the checkpoint: out = (scale*codes) T_0 + sum_t c_t v_t.
+ * precompute_grouped selects one precompute workgroup per key head (k read
+ * once for the GQA group) instead of one per value head; results are equal.
+ * block_kc is accepted for signature parity and must be 128 or K.
+ * Replaces gdn_replay_fp8_split, prototype/gdn_replayssm_fp8_kernel.py:1129-1235
+ * (device work: same file :798-1126).
+ */
+int gdnr_replay_fp8_split(const gdnr_tensor* checkpoint, const gdnr_tensor* checkpoint_scale,
+                          const gdnr_tensor* q, const gdnr_tensor* k_cache,
+                          const gdnr_tensor* v_cache, const gdnr_tensor* g_cache,
+                          const gdnr_tensor* beta_cache, const gdnr_tensor* valid_len,
+                          const gdnr_tensor* transformed_query,
+                          const gdnr_tensor* coefficient, const gdnr_tensor* out,
+                          int32_t block_v, int32_t block_kc, int32_t precompute_grouped,
+                          void* stream);
+
+/*
+ * Full-contract preparation of one token per sequence:
+ *   q,k <- x / sqrt(sum(x^2) + 1e-6) (per key head), q -> q_out[b],
+ *   k -> k_ring[b, pos[b]], v (copied) -> v_ring[b, pos[b]],
+ *   g = -exp(A_log) * softplus_20(a + dt_bias) -> g_ring[b, pos[b]],
+ *   beta = sigmoid(b) -> beta_ring[b, pos[b]].
+ * Shapes: mixed_qkv [B, 2*H*K + HV*V] (row stride free, unit inner stride);
+ *   a, b [B,HV] bf16|f16|f32; a_log, dt_bias [HV] bf16|f16|f32; pos [B]
+ *   i32|i64; q_out [B,H,K]; k_ring [B,L,H,K]; v_ring [B,L,HV,V];
+ *   g_ring, beta_ring [B,L,HV]. mixed_qkv, q_out, k_ring, v_ring share a dtype.
+ * `fused` is accepted for signature parity (0 and 1 run the same kernel).
+ * beta_ring is addressed with its own strides (the reference reuses
+ * g_ring's, kernel:570-575; identical whenever the two rings match).
+ * Replaces gdn_prep_ring, prototype/gdn_replayssm_fp8_kernel.py:710-795
+ * (device work: same file :453-707).
+ */
+int gdnr_prep_ring(const gdnr_tensor* mixed_qkv, const gdnr_tensor* a, const gdnr_tensor* b,
+                   const gdnr_tensor* a_log, const gdnr_tensor* dt_bias,
+                   const gdnr_tensor* pos, const gdnr_tensor* q_out,
+                   const gdnr_tensor* k_ring, const gdnr_tensor* v_ring,
+                   const gdnr_tensor* g_ring, const gdnr_tensor* beta_ring,
+                   int32_t fused, void* stream);
+
+/*
+ * The whole full-contract decode step in ONE launch: gdnr_prep_ring followed
+ * by gdnr_replay_fp8 on the same buffers, with results identical to that
+ * pair (the freshly appended token is taken from registers, rounded to the
+ * ring dtype exactly as the ring stores it).
+ * Composes prep_step + gdn_replay_fp8 as sequenced by
+ * prototype/bench_gdn_full_contract.py:138-154,246-297.
+ */
+int gdnr_prep_replay_fp8(const gdnr_tensor* mixed_qkv, const gdnr_tensor* a,
+                         const gdnr_tensor* b, const gdnr_tensor* a_log,
+                         const gdnr_tensor* dt_bias, const gdnr_tensor* pos,
+                         const gdnr_tensor* checkpoint, const gdnr_tensor* checkpoint_scale,
+                         const gdnr_tensor* q_out, const gdnr_tensor* k_ring,
+                         const gdnr_tensor* v_ring, const gdnr_tensor* g_ring,
+                         const gdnr_tensor* beta_ring, const gdnr_tensor* valid_len,
+                         const gdnr_tensor* flush, const gdnr_tensor* out,
+                         int32_t block_v, void* stream);
+
+/*
+ * vblock32 quantiser, bit-exact with the reference's
+ *   scale = fp16(amax/448) if amax > 0 else 1;  codes = e4m3fn(clamp(x/scale, +-448))
+ * state [B,HV,V,K] f32 -> payload [B,HV,V,K] fp8|u8, scale [B,HV,V/32] f16|f32.
+ * saturated (optional, may be NULL) [B,HV,V/32] i32 receives the per-vblock
+ * count of |x/scale| > 448.
+ * Replaces quantize_checkpoint(state, "vblock", 32),
+ * prototype/gdn_replay_fp8_reference.py:40-106 (vblock branch :71-87, :91-99).
+ */
+int gdnr_quantize_vblock32(const gdnr_tensor* state, const gdnr_tensor* payload,
+                           const gdnr_tensor* scale, const gdnr_tensor* saturated,
+                           void* stream);
+
+/*
+ * state = float(payload) * float(scale) per vblock32.
+ * Replaces dequantize_checkpoint, prototype/gdn_replay_fp8_reference.py:109-134.
+ */
+int gdnr_dequantize_vblock32(const gdnr_tensor* payload, const gdnr_tensor* scale,
+                             const gdnr_tensor* state, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GDNR_H */

@@ -1,0 +1,59 @@
+"""Shared helpers of the GPU parity tests: build device inputs with the
+synthetic generator and hand the same values to the CPU oracle."""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+import gdn_replayssm_fp8_kernel as gk
+import gdn_replayssm_synth as synth
+from oracle import fp8_quant, gdn_oracle
+
+STORAGE = {torch.bfloat16: "bf16", torch.float16: "f16", torch.float32: "f32"}
+
+
+def np32(t: torch.Tensor) -> np.ndarray:
+    return t.detach().float().cpu().numpy()
+
+
+def codes_np(payload: torch.Tensor) -> np.ndarray:
+    return payload.detach().view(torch.uint8).cpu().numpy()
+
+
+def make_replay_case(batch, ring_len, device, seed=0, heads=16, value_heads=32, dtype=torch.bfloat16,
+                     warmup=32, valid=None, flush=None):
+    """Checkpoint (device-quantised), ring, q, valid_len, flush for one replay call."""
+    shape = synth.Shape(batch, heads, value_heads)
+    gen = synth.generator(seed, device)
+    a_log, dt_bias = synth.gating_params(shape, gen, device)
+    state = synth.warm_state(shape, warmup, gen, device, a_log, dt_bias)
+    ckpt = gk.quantize_checkpoint(state)
+    q, k, v, g, beta = synth.ring_inputs(shape, ring_len, gen, device, a_log, dt_bias, dtype)
+    if valid is None:
+        valid = torch.randint(1, ring_len + 1, (batch,), generator=gen, device=device, dtype=torch.int32)
+    else:
+        valid = torch.as_tensor(valid, dtype=torch.int32, device=device)
+    if flush is None:
+        flush = torch.zeros(batch, dtype=torch.bool, device=device)
+    else:
+        flush = torch.as_tensor(flush, dtype=torch.bool, device=device)
+    return dict(state=state, ckpt=ckpt, q=q, k=k, v=v, g=g, beta=beta, valid=valid, flush=flush)
+
+
+def oracle_replay(case, dtype=np.float64):
+    """Oracle output (float) and new codes/scale for a replay call on `case`."""
+    return gdn_oracle.replay_step(codes_np(case["ckpt"].payload), case["ckpt"].scale.cpu().numpy(),
+                                  np32(case["q"]), np32(case["k"]), np32(case["v"]), np32(case["g"]),
+                                  np32(case["beta"]), case["valid"].cpu().numpy(), case["flush"].cpu().numpy(),
+                                  dtype)
+
+
+def run_replay(case, block_v=128, out=None):
+    return gk.gdn_replay_fp8(case["ckpt"].payload, case["ckpt"].scale, case["q"], case["k"], case["v"],
+                             case["g"], case["beta"], case["valid"], case["flush"], block_v=block_v, out=out)
+
+
+def c_quantize(state: torch.Tensor):
+    codes, scale, sat = fp8_quant.quantize_vblock32(np32(state))
+    return codes, scale, sat
