@@ -75,11 +75,11 @@ int gdnr_abi_version(void);
  *   flush[b] != 0: forward rebuild of the state over the same tokens, writes
  *                  out[b] from the rebuilt fp32 state, then requantises it to
  *                  vblock32 IN PLACE (checkpoint[b], checkpoint_scale[b]).
- * Shapes: checkpoint [B,HV,V,K] fp8/u8; checkpoint_scale [B,HV,V/32] f16|f32;
+ * Shapes: checkpoint [B,HV,V,K] fp8/u8; checkpoint_scale [B,HV,V/32] f16;
  *   q [B,H,K]; k_cache [B,L,H,K]; v_cache [B,L,HV,V]; g_cache, beta_cache
- *   [B,L,HV]; valid_len [B] i32|i64; flush [B] bool|u8|i32; out [B,HV,V].
- *   q, k_cache, v_cache and out share one dtype (bf16|f16|f32); g and beta
- *   may each be bf16|f16|f32. K == 128, V % 32 == 0, HV % H == 0, L <= 64.
+ *   [B,L,HV]; valid_len [B] i32; flush [B] bool|u8; out [B,HV,V].
+ *   q, k_cache, v_cache, g_cache, beta_cache and out share one dtype
+ *   (bf16|f16|f32). K == 128, V % 32 == 0, HV % H == 0, 1 <= L <= 64.
  * block_v (32|64|128, dividing V) is the number of V-rows one workgroup
  *   streams; unlike the reference it does not constrain the flush.
  * Replaces gdn_replay_fp8, prototype/gdn_replayssm_fp8_kernel.py:344-405
@@ -120,8 +120,8 @@ int gdnr_replay_fp8_split(const gdnr_tensor* checkpoint, const gdnr_tensor* chec
  *   g = -exp(A_log) * softplus_20(a + dt_bias) -> g_ring[b, pos[b]],
  *   beta = sigmoid(b) -> beta_ring[b, pos[b]].
  * Shapes: mixed_qkv [B, 2*H*K + HV*V] (row stride free, unit inner stride);
- *   a, b [B,HV] bf16|f16|f32; a_log, dt_bias [HV] bf16|f16|f32; pos [B]
- *   i32|i64; q_out [B,H,K]; k_ring [B,L,H,K]; v_ring [B,L,HV,V];
+ *   a, b [B,HV] f32 or the ring dtype; a_log, dt_bias [HV] f32; pos [B]
+ *   i32; q_out [B,H,K]; k_ring [B,L,H,K]; v_ring [B,L,HV,V];
  *   g_ring, beta_ring [B,L,HV]. mixed_qkv, q_out, k_ring, v_ring share a dtype.
  * `fused` is accepted for signature parity (0 and 1 run the same kernel).
  * beta_ring is addressed with its own strides (the reference reuses

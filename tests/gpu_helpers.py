@@ -38,12 +38,17 @@ def make_replay_case(batch, ring_len, device, seed=0, heads=16, value_heads=32, 
         flush = torch.zeros(batch, dtype=torch.bool, device=device)
     else:
         flush = torch.as_tensor(flush, dtype=torch.bool, device=device)
-    return dict(state=state, ckpt=ckpt, q=q, k=k, v=v, g=g, beta=beta, valid=valid, flush=flush)
+    # host snapshot of the checkpoint as created: a flush rewrites ckpt in place
+    codes0 = codes_np(ckpt.payload).copy()
+    scale0 = ckpt.scale.cpu().numpy().copy()
+    return dict(state=state, ckpt=ckpt, codes0=codes0, scale0=scale0, q=q, k=k, v=v, g=g, beta=beta, valid=valid,
+                flush=flush)
 
 
 def oracle_replay(case, dtype=np.float64):
-    """Oracle output (float) and new codes/scale for a replay call on `case`."""
-    return gdn_oracle.replay_step(codes_np(case["ckpt"].payload), case["ckpt"].scale.cpu().numpy(),
+    """Oracle output (float) and new codes/scale for a replay call on `case`,
+    started from the checkpoint as it was when the case was made."""
+    return gdn_oracle.replay_step(case["codes0"], case["scale0"],
                                   np32(case["q"]), np32(case["k"]), np32(case["v"]), np32(case["g"]),
                                   np32(case["beta"]), case["valid"].cpu().numpy(), case["flush"].cpu().numpy(),
                                   dtype)

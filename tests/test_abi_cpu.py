@@ -1,0 +1,186 @@
+"""The C-ABI library on the CPU: it loads, exports every symbol include/gdnr.h
+declares, and rejects misuse on the host before any HIP call.
+
+Every call here fails validation (or has batch 0), so no kernel is launched
+and no GPU is needed; the descriptors carry fake, never-dereferenced device
+addresses. The reference wrappers validate nothing
+(prototype/gdn_replayssm_fp8_kernel.py:344-405,710-795,1129-1235).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+import subprocess
+
+import pytest
+import torch
+
+import gdnr_lib
+from conftest import REPO
+
+OK, INVALID, UNSUPPORTED = 0, 1, 2
+BF16, F16, F32, FP8, U8, I32, I64, BOOL = range(8)
+FAKE = 0x7F0000000000  # 256-byte aligned, never dereferenced
+
+
+def desc(shape, dtype, data=FAKE, strides=None):
+    t = gdnr_lib.GdnrTensor()
+    t.data = data or None
+    t.dtype = dtype
+    t.ndim = len(shape)
+    if strides is None:
+        strides, acc = [], 1
+        for s in reversed(shape):
+            strides.insert(0, acc)
+            acc *= s
+    for d, (s, st) in enumerate(zip(shape, strides)):
+        t.shape[d] = s
+        t.strides[d] = st
+    return t
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return gdnr_lib.load_library()
+
+
+def declared_functions() -> list[str]:
+    header = (REPO / "include" / "gdnr.h").read_text()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\*?\s+\**(gdnr_\w+)\s*\(", header, flags=re.M)))
+
+
+def test_every_declared_symbol_is_exported(lib):
+    names = declared_functions()
+    assert len(names) >= 8, names
+    out = subprocess.run(["nm", "-D", "--defined-only", str(gdnr_lib.LIBRARY_PATH)], capture_output=True, text=True,
+                         check=True).stdout
+    exported = set(re.findall(r"\bT (gdnr_\w+)$", out, flags=re.M))
+    missing = [n for n in names if n not in exported]
+    assert not missing, missing
+    for name in names:
+        assert hasattr(lib, name)
+    assert set(gdnr_lib.ENTRY_POINTS) <= set(names)
+
+
+def test_abi_version(lib):
+    assert lib.gdnr_abi_version() == gdnr_lib.ABI_VERSION
+
+
+class ReplayCase:
+    """A valid gdnr_replay_fp8 argument set at B=2, H=2, HV=4, L=4 (bf16);
+    tests break one argument at a time."""
+
+    def __init__(self, B=2, H=2, HV=4, K=128, V=128, L=4):
+        self.t = {
+            "checkpoint": desc([B, HV, V, K], FP8),
+            "checkpoint_scale": desc([B, HV, V // 32], F16),
+            "q": desc([B, H, K], BF16),
+            "k_cache": desc([B, L, H, K], BF16),
+            "v_cache": desc([B, L, HV, V], BF16),
+            "g_cache": desc([B, L, HV], BF16),
+            "beta_cache": desc([B, L, HV], BF16),
+            "valid_len": desc([B], I32),
+            "flush": desc([B], BOOL),
+            "out": desc([B, HV, V], BF16),
+        }
+        self.block_v = 128
+
+    def call(self, lib):
+        ptrs = [ctypes.byref(self.t[k]) for k in ("checkpoint", "checkpoint_scale", "q", "k_cache", "v_cache",
+                                                  "g_cache", "beta_cache", "valid_len", "flush", "out")]
+        rc = lib.gdnr_replay_fp8(*ptrs, self.block_v, None)
+        return rc, lib.gdnr_last_error().decode()
+
+
+@pytest.mark.parametrize("mutate,code,needle", [
+    (lambda c: c.t.__setitem__("checkpoint", desc([2, 4, 128, 64], FP8)), INVALID, "checkpoint"),
+    (lambda c: c.t.__setitem__("k_cache", desc([2, 4, 2, 64], BF16)), UNSUPPORTED, "K=64"),
+    (lambda c: c.t.__setitem__("checkpoint_scale", desc([2, 4, 4], F32)), INVALID, "checkpoint_scale"),
+    (lambda c: c.t.__setitem__("valid_len", desc([2], I64)), INVALID, "valid_len"),
+    (lambda c: c.t.__setitem__("flush", desc([3], BOOL)), INVALID, "flush"),
+    (lambda c: c.t.__setitem__("q", desc([2, 2, 128], F16)), INVALID, "q"),
+    (lambda c: c.t.__setitem__("out", desc([2, 4, 96], BF16)), INVALID, "out"),
+    (lambda c: c.t.__setitem__("g_cache", desc([2, 4, 4], F32)), UNSUPPORTED, "g_cache"),
+    (lambda c: c.t.__setitem__("checkpoint", desc([2, 4, 128, 128], FP8, data=FAKE + 8)), INVALID, "aligned"),
+    (lambda c: c.t.__setitem__("k_cache", desc([2, 4, 2, 128], BF16, strides=[1024, 256, 128, 2])), INVALID,
+     "innermost"),
+    (lambda c: setattr(c, "block_v", 48), INVALID, "block_v"),
+    (lambda c: c.t.__setitem__("checkpoint", desc([2, 4, 128, 128], F32)), INVALID, "checkpoint"),
+    (lambda c: c.t.__setitem__("q", desc([2, 2, 128], BF16, data=0)), INVALID, "null data"),
+])
+def test_replay_rejects_misuse(lib, mutate, code, needle):
+    case = ReplayCase()
+    mutate(case)
+    rc, msg = case.call(lib)
+    assert rc == code, msg
+    assert needle in msg, msg
+
+
+def test_ring_longer_than_built_is_unsupported(lib):
+    case = ReplayCase(L=65)
+    rc, msg = case.call(lib)
+    assert rc == UNSUPPORTED and "ring length" in msg
+
+
+def test_value_heads_must_be_a_multiple_of_key_heads(lib):
+    rc, msg = ReplayCase(H=2, HV=3).call(lib)
+    assert rc == INVALID and "multiple of key heads" in msg
+
+
+def test_empty_batch_is_a_no_op(lib):
+    case = ReplayCase(B=0)
+    rc, msg = case.call(lib)
+    assert rc == OK and msg == ""
+
+
+def test_prep_rejects_narrow_mixed_qkv(lib):
+    B, H, HV, K, V, L = 2, 2, 4, 128, 128, 4
+    args = [desc([B, 2 * H * K + HV * V - 8], BF16), desc([B, HV], BF16), desc([B, HV], BF16), desc([HV], F32),
+            desc([HV], F32), desc([B], I32), desc([B, H, K], BF16), desc([B, L, H, K], BF16),
+            desc([B, L, HV, V], BF16), desc([B, L, HV], BF16), desc([B, L, HV], BF16)]
+    rc = lib.gdnr_prep_ring(*[ctypes.byref(a) for a in args], 1, None)
+    assert rc == INVALID and "mixed_qkv" in lib.gdnr_last_error().decode()
+    args[0] = desc([B, 2 * H * K + HV * V], BF16)
+    args[3] = desc([HV], BF16)                           # A_log must be f32
+    rc = lib.gdnr_prep_ring(*[ctypes.byref(a) for a in args], 1, None)
+    assert rc == INVALID and "a_log" in lib.gdnr_last_error().decode()
+
+
+def test_split_rejects_short_coefficient_buffer(lib):
+    case = ReplayCase()
+    t = case.t
+    tq = desc([2, 4, 128], F32)
+    coef = desc([2, 4, 3], F32)                          # ring is 4 long
+    ptrs = [ctypes.byref(t[k]) for k in ("checkpoint", "checkpoint_scale", "q", "k_cache", "v_cache", "g_cache",
+                                         "beta_cache", "valid_len")]
+    rc = lib.gdnr_replay_fp8_split(*ptrs, ctypes.byref(tq), ctypes.byref(coef), ctypes.byref(t["out"]), 128, 128, 1,
+                                   None)
+    assert rc == INVALID and "coefficient_buffer" in lib.gdnr_last_error().decode()
+
+
+def test_quantize_rejects_wrong_key_dim(lib):
+    rc = lib.gdnr_quantize_vblock32(ctypes.byref(desc([1, 2, 32, 64], F32)), ctypes.byref(desc([1, 2, 32, 64], FP8)),
+                                    ctypes.byref(desc([1, 2, 1], F16)), None, None)
+    assert rc == UNSUPPORTED and "K=64" in lib.gdnr_last_error().decode()
+
+
+def test_last_error_is_cleared_by_a_good_call(lib):
+    ReplayCase(L=65).call(lib)
+    assert lib.gdnr_last_error().decode() != ""
+    rc, msg = ReplayCase(B=0).call(lib)
+    assert rc == OK and msg == ""
+
+
+def test_python_wrappers_refuse_host_tensors():
+    """The drop-in functions never fall back to a CPU path."""
+    import gdn_replayssm_fp8_kernel as gk
+
+    B, H, HV, L = 1, 1, 2, 2
+    z = lambda *s, dtype=torch.bfloat16: torch.zeros(*s, dtype=dtype)
+    with pytest.raises(ValueError, match="GPU"):
+        gk.gdn_replay_fp8(z(B, HV, 128, 128, dtype=torch.float8_e4m3fn), z(B, HV, 4, dtype=torch.float16),
+                          z(B, H, 128), z(B, L, H, 128), z(B, L, HV, 128), z(B, L, HV), z(B, L, HV),
+                          z(B, dtype=torch.int32), z(B, dtype=torch.bool))
+    with pytest.raises(ValueError, match="GPU"):
+        gk.quantize_checkpoint(torch.zeros(1, 1, 32, 128))

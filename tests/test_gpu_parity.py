@@ -28,7 +28,7 @@ OUT_TOL = 2e-3
 
 def test_fp8_decode_all_codes(device):
     """Every e4m3fn code decodes on the device to the OCP value (scale 1)."""
-    codes = torch.arange(256, dtype=torch.int32).to(torch.uint8).repeat(8 * 32 * 128 // 256)
+    codes = torch.arange(256, dtype=torch.int32).to(torch.uint8).repeat(32 * 128 // 256)
     payload = codes.view(1, 1, 32, 128).to(device).view(torch.float8_e4m3fn)
     scale = torch.ones(1, 1, 1, dtype=torch.float16, device=device)
     ck = gk.QuantizedCheckpoint(payload, scale, "vblock", 32, 0.0)
@@ -136,6 +136,20 @@ def test_flush_matches_oracle(device, ring_len, block_v):
     deq_ref = gdn_oracle.dequantize_vblock32(ref_codes, ref_scale)
     assert rel_l2(deq, deq_ref) < 2e-3
     assert np.mean(case["ckpt"].scale.cpu().numpy() != ref_scale) < 0.02
+
+
+@pytest.mark.parametrize("ring_len,block_v", [(4, 32), (16, 64), (64, 128)])
+def test_flush_output_equals_replay_output(device, ring_len, block_v):
+    """Invariant: the adjoint replay (flush = 0) and the forward rebuild
+    (flush = 1) compute the same o = S q from the same checkpoint and ring, for
+    every ring fill 0..L; only fp32 summation order differs."""
+    valid = sorted(set([0, 1, 2, ring_len // 2, ring_len - 1, ring_len]))
+    case = make_replay_case(len(valid), ring_len, device, seed=8, valid=valid, flush=[0] * len(valid))
+    replay_out = np32(run_replay(case, block_v=block_v))
+    case["flush"] = torch.ones(len(valid), dtype=torch.bool, device=device)
+    flush_out = np32(run_replay(case, block_v=block_v))
+    for i in range(len(valid)):
+        assert rel_l2(flush_out[i], replay_out[i]) < 2e-3, (valid[i], rel_l2(flush_out[i], replay_out[i]))
 
 
 @pytest.mark.parametrize("act", [torch.float16, torch.float32])
