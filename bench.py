@@ -1,0 +1,297 @@
+"""Benchmark of the ReplaySSM GDN decode path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--batch 64] [--window 16]
+
+Workload (BASELINE config 2 at its headline cell): the full-contract decode
+step of one Qwen3.5-4B GDN layer (H=16, HV=32, K=V=128), batch 64, ring
+window L=16, from raw bf16 mixed_qkv / a / b. A step is ONE launch of the
+fused prep + replay kernel (gdn_prep_replay_fp8): q/k L2 norm, gating, ring
+append, then the adjoint replay against the FP8 vblock32 checkpoint -- or, on
+the ring's last slot, the forward rebuild + in-place requantisation (flush).
+The batch runs the reference's cycle (prototype/bench_gdn_full_contract.py
+:225-308): all sequences at ring fill l = 1..L, flushing at l = L, so the
+per-step time is amortised over whole ring cycles.
+
+Measurement:
+  * BUFFER_SETS independent checkpoint + ring sets (~47 MB each at B=64) are
+    used round-robin, one set per step, so consecutive steps never hit the
+    256 MB Infinity Cache with the previous step's data; each set still runs
+    a coherent cycle (set = step % S, fill = (step // S) % L + 1).
+  * The steps are captured into a HIP graph (torch.cuda.CUDAGraph) once per
+    round of S*L steps and replayed: no host launch overhead in the timed
+    region. Timed = exactly `steps` launches (rounded up to whole rounds so
+    the cycle amortisation is exact; the JSON reports the number timed).
+  * HIP events on the launch stream bracket the timed region; `value` is
+    microseconds per decode step (lower is better).
+  * roofline: algorithmic bytes per step (every compulsory tensor element
+    counted once; gdn_replayssm_traffic.cycle_bytes_per_step) / average launch
+    duration, against 8 TB/s.
+  * cpu_baseline: the reference's host algorithm (oracle/cpu_torch_path.py:
+    dequantise -> forward replay -> emit, requantise on flush) in fp32 torch on
+    the host cores, over one whole ring cycle of a batch sample, scaled to the
+    full batch.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+PKG = REPO / "fp8-replayssm-gdn-kernel_amd"
+for _p in (REPO, PKG):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+METRIC = "µs per GDN-layer decode step (B=64, L=16) + achieved HBM GB/s % of peak"
+HBM_PEAK_GBS = 8000.0
+KERNEL_NAME = "replay_kernel<ActBF16, 16, kModeFused, false>"
+CPU_SAMPLE_SECONDS = 10.0
+CPU_MAX_CYCLES = 8
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def parse_args():
+    p = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=3840)
+    p.add_argument("--warmup", type=int, default=384)
+    p.add_argument("--batch", type=int, default=64)
+    p.add_argument("--window", type=int, default=16)
+    p.add_argument("--block-v", type=int, default=128)
+    p.add_argument("--sets", type=int, default=12, help="rotating buffer sets (defeats the Infinity Cache)")
+    p.add_argument("--phase", choices=("lockstep", "mixed"), default="lockstep",
+                   help="lockstep: the reference's cycle; mixed: sequence b at ring phase b %% L")
+    p.add_argument("--cpu-sample", type=int, default=64, help="batch of the CPU-baseline sample (0: skip)")
+    p.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a HIP graph")
+    p.add_argument("--profile", action="store_true",
+                   help="short run for rocprofv3: no CPU baseline, few rounds")
+    return p.parse_args()
+
+
+def traffic_from_profiles(batch: int, window: int):
+    """HBM bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE +
+    WRITE_SIZE, calibrated against a copy kernel), as recorded in profiles/."""
+    path = REPO / "profiles" / f"traffic_fused_b{batch}_l{window}.json"
+    if not path.exists():
+        return None
+    try:
+        return json.loads(path.read_text()).get("bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def cpu_baseline(args, shape, window):
+    """Time the reference's host path on a batch sample; scale to the full batch."""
+    import torch
+
+    from oracle import cpu_torch_path
+
+    sample = max(1, min(args.cpu_sample, args.batch))
+    gen = torch.Generator().manual_seed(1)
+    B, H, HV, K, V = sample, shape.heads, shape.value_heads, shape.key_dim, shape.value_dim
+    state = torch.randn(B, HV, V, K, generator=gen) * 0.02
+    codes, scale = cpu_torch_path.quantize_vblock32(state)
+    a_log = torch.rand(HV, generator=gen) * math.log(16.0)
+    dt_bias = torch.zeros(HV)
+    dec = cpu_torch_path.HostDecoder(codes, scale, a_log, dt_bias, H, window)
+    width = 2 * H * K + HV * V
+    mixed = torch.randn(window, B, width, generator=gen).to(torch.bfloat16)
+    ab = torch.randn(window, 2, B, HV, generator=gen).to(torch.bfloat16)
+    threads = torch.get_num_threads()
+    dec.step(mixed[0], ab[0, 0], ab[0, 1])          # warm the allocator / thread pool
+    dec = cpu_torch_path.HostDecoder(codes, scale, a_log, dt_bias, H, window)
+    t0 = time.perf_counter()
+    cycles = 0
+    while True:                                      # whole cycles, >= CPU_SAMPLE_SECONDS of work
+        for t in range(window):
+            dec.step(mixed[t], ab[t, 0], ab[t, 1])
+        cycles += 1
+        elapsed = time.perf_counter() - t0
+        if elapsed >= CPU_SAMPLE_SECONDS or cycles >= CPU_MAX_CYCLES:
+            break
+    us_per_step = elapsed / (cycles * window) * 1e6 * (args.batch / sample)
+    scaled = f"; scaled x{args.batch / sample:g} to batch {args.batch}" if sample != args.batch else ""
+    return {
+        "value": us_per_step,
+        "unit": "us/step",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"{cycles} whole ring cycle(s) ({cycles * window} steps incl. {cycles} flushes) at batch {sample}, "
+                   f"same layer shape and cycle as the GPU run, fp32 torch on {threads} host threads, "
+                   f"{elapsed:.2f} s{scaled}"),
+    }
+
+
+def main() -> int:
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported (the ReplaySSM path shards "
+              "by sequence with no communication; run one process per GPU).", file=sys.stderr)
+        return 2
+
+    import torch
+
+    import gdn_replayssm_fp8_kernel as gk
+    import gdn_replayssm_synth as synth
+    from gdn_replayssm_traffic import LayerShape, bf16_rmw_bytes, cycle_bytes_per_step, reference_traffic
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU (the HIP path has no CPU fallback)", file=sys.stderr)
+        return 1
+    device = torch.device("cuda:0")
+    torch.cuda.set_device(device)
+    B, L, S = args.batch, args.window, args.sets
+    shape = synth.Shape(B)
+    traffic_shape = LayerShape(B)
+    round_len = S * L
+    if args.profile:
+        args.steps, args.warmup = 2 * round_len, round_len
+    rounds = max(1, math.ceil(args.steps / round_len))
+    warm_rounds = max(1, math.ceil(args.warmup / round_len))
+    steps = rounds * round_len
+    log(f"[bench] B={B} L={L} sets={S} block_v={args.block_v} phase={args.phase}: "
+        f"{rounds} timed rounds of {round_len} steps ({steps} steps), {warm_rounds} warm-up rounds")
+
+    # ---- inputs resident in HBM ----------------------------------------------
+    gen = synth.generator(0, device)
+    a_log, dt_bias = synth.gating_params(shape, gen, device)
+    t0 = time.perf_counter()
+    state = synth.warm_state(shape, 256, gen, device, a_log, dt_bias)
+    ck = gk.quantize_checkpoint(state, saturation=False)
+    del state
+    mixed, a_raw, b_raw = synth.raw_step_inputs(shape, L, gen, device)
+    mixed = [mixed[:, t].contiguous() for t in range(L)]
+    a_raw = [a_raw[:, t].contiguous() for t in range(L)]
+    b_raw = [b_raw[:, t].contiguous() for t in range(L)]
+    sets = []
+    for _ in range(S):
+        sets.append(dict(
+            payload=ck.payload.clone(), scale=ck.scale.clone(),
+            q_out=torch.zeros(B, shape.heads, 128, dtype=torch.bfloat16, device=device),
+            k=torch.zeros(B, L, shape.heads, 128, dtype=torch.bfloat16, device=device),
+            v=torch.zeros(B, L, shape.value_heads, 128, dtype=torch.bfloat16, device=device),
+            g=torch.zeros(B, L, shape.value_heads, dtype=torch.bfloat16, device=device),
+            beta=torch.zeros(B, L, shape.value_heads, dtype=torch.bfloat16, device=device),
+            out=torch.empty(B, shape.value_heads, 128, dtype=torch.bfloat16, device=device)))
+    # per-step metadata, one variant per position in the cycle
+    seq = torch.arange(B, device=device)
+    meta = []
+    for i in range(L):
+        phase = (seq % L) if args.phase == "mixed" else torch.zeros_like(seq)
+        fill = ((phase + i) % L + 1).to(torch.int32)
+        meta.append(dict(pos=(fill - 1).contiguous(), valid=fill.contiguous(), flush=(fill == L).contiguous()))
+    torch.cuda.synchronize()
+    log(f"[bench] inputs ready in {time.perf_counter() - t0:.1f} s "
+        f"({torch.cuda.memory_allocated() / 2**30:.2f} GiB allocated)")
+
+    def launch(i: int) -> None:
+        st = sets[i % S]
+        c = (i // S) % L
+        m = meta[c]
+        gk.gdn_prep_replay_fp8(mixed[c], a_raw[c], b_raw[c], a_log, dt_bias, m["pos"], st["payload"], st["scale"],
+                               st["q_out"], st["k"], st["v"], st["g"], st["beta"], m["valid"], m["flush"],
+                               block_v=args.block_v, out=st["out"])
+
+    def one_round() -> None:
+        for i in range(round_len):
+            launch(i)
+
+    # fill every ring once (also compiles nothing: kernels are prebuilt)
+    one_round()
+    torch.cuda.synchronize()
+
+    stream = torch.cuda.Stream(device)       # default priority
+    graph = None
+    if not args.no_graph:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(stream):
+            one_round()                       # warm this stream before capture
+            stream.synchronize()
+            with torch.cuda.graph(graph, stream=stream):
+                one_round()
+        torch.cuda.synchronize()
+
+    def run_rounds(n: int) -> None:
+        with torch.cuda.stream(stream):
+            for _ in range(n):
+                if graph is not None:
+                    graph.replay()
+                else:
+                    one_round()
+
+    run_rounds(warm_rounds)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    wall0 = time.perf_counter()
+    start.record(stream)
+    run_rounds(rounds)
+    end.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    ms_total = start.elapsed_time(end)
+    us_step = ms_total * 1e3 / steps
+    log(f"[bench] timed {steps} steps: {us_step:.3f} us/step (events), wall {wall * 1e6 / steps:.3f} us/step")
+
+    bytes_step = cycle_bytes_per_step(traffic_shape, L, with_prep=True)
+    achieved = bytes_step / (us_step * 1e-6) / 1e9
+    result = {
+        "metric": METRIC,
+        "value": round(us_step, 4),
+        "unit": "us/step",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warm_rounds * round_len,
+        "ms_per_step": us_step / 1e3,
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "storage": "fp8-e4m3fn checkpoint (fp16 vblock32 scales), bf16 ring/q/out",
+        "data": "synthetic (seeded; BASELINE distributions, 256-step warm-up state)",
+        "config": {
+            "workload": (f"full-contract decode step (prep + replay, flush at l=L), one fused launch per step, "
+                         f"Qwen3.5-4B GDN layer H=16 HV=32 K=V=128, B={B}, L={L}, cycle-amortised ({args.phase} "
+                         f"ring phases), {S} rotating buffer sets"),
+            "batch": B, "window": L, "block_v": args.block_v, "buffer_sets": S, "phase": args.phase,
+            "hip_graph": graph is not None,
+        },
+        "seq_per_s": B / (us_step * 1e-6),
+        "algorithmic_bytes_per_step": bytes_step,
+        "roofline": {
+            "bound": "hbm",
+            "kernel": KERNEL_NAME,
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic_from_profiles(B, L),
+        },
+        "bytes_vs_bf16_rmw": {
+            "bf16_rmw_bytes_per_step": bf16_rmw_bytes(traffic_shape),
+            "ratio_cycle_avg": bf16_rmw_bytes(traffic_shape) / bytes_step,
+            "ratio_reference_accounting": bf16_rmw_bytes(traffic_shape)
+            / reference_traffic(traffic_shape, L, args.block_v)["replay_logical"],
+        },
+        "wall_us_per_step": wall * 1e6 / steps,
+    }
+    if args.cpu_sample > 0 and not args.profile:
+        log("[bench] timing the CPU baseline ...")
+        result["cpu_baseline"] = cpu_baseline(args, traffic_shape, L)
+        result["cpu_baseline"]["gpu_speedup"] = result["cpu_baseline"]["value"] / us_step
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

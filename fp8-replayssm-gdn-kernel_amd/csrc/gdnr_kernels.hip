@@ -262,7 +262,7 @@ __global__ __launch_bounds__(256) void replay_kernel(const ReplayArgs a) {
     const float q0 = Act::round(q_raw.x / qd), q1 = Act::round(q_raw.y / qd);
     const float k0 = Act::round(k_raw.x / kd), k1 = Act::round(k_raw.y / kd);
     const float xg = a_raw + dtb_raw;
-    const float sp = xg <= 20.0f ? log1pf(expf(xg)) : xg;
+    const float sp = xg <= 20.0f ? logf(1.0f + expf(xg)) : xg;  // kernel:560, as written there
     const float gate = Act::round(-expf(alog_raw) * sp);
     const float bet = Act::round(1.0f / (1.0f + expf(-b_raw)));
     if (wave == 0) Act::st2(lds + a.lds_q + 2 * lane * ES, q0, q1);
@@ -542,7 +542,7 @@ __global__ __launch_bounds__(256) void prep_kernel(const PrepArgs a) {
     }
     if (lane == 0) {
       const float x = ld_gate<GATE_F32, Act>(a.a, (int64_t)b * a.a_b + (int64_t)hv * a.a_h) + a.dt_bias[(int64_t)hv * a.db_s];
-      const float sp = x <= 20.0f ? log1pf(expf(x)) : x;
+      const float sp = x <= 20.0f ? logf(1.0f + expf(x)) : x;  // kernel:560, as written there
       const float gate = -expf(a.a_log[(int64_t)hv * a.al_s]) * sp;
       const float bet = 1.0f / (1.0f + expf(-ld_gate<GATE_F32, Act>(a.bgate, (int64_t)b * a.bg_b + (int64_t)hv * a.bg_h)));
       Act::st(a.g, (int64_t)b * a.g_b + (int64_t)pos * a.g_t + (int64_t)hv * a.g_h, gate);

@@ -425,10 +425,11 @@ def replay_step(codes, scale, q, k_cache, v_cache, g_cache, beta_cache, valid_le
 # --------------------------------------------------------------------------
 
 def softplus_thresholded(x):
-    """kernel:560: log(1 + exp(x)) for x <= 20, else x."""
+    """kernel:560: log(1 + exp(x)) for x <= 20, else x -- the formula as the
+    reference kernel writes it (not log1p), evaluated here in float64."""
     x = np.asarray(x, dtype=np.float64)
     with np.errstate(over="ignore"):
-        return np.where(x <= SOFTPLUS_THRESHOLD, np.log1p(np.exp(np.minimum(x, SOFTPLUS_THRESHOLD))), x)
+        return np.where(x <= SOFTPLUS_THRESHOLD, np.log(1.0 + np.exp(np.minimum(x, SOFTPLUS_THRESHOLD))), x)
 
 
 def prep_values(mixed_qkv, a, b, a_log, dt_bias, heads, key_dim, value_heads, value_dim):
