@@ -50,7 +50,7 @@ for _p in (REPO, PKG):
 
 METRIC = "µs per GDN-layer decode step (B=64, L=16) + achieved HBM GB/s % of peak"
 HBM_PEAK_GBS = 8000.0
-KERNEL_NAME = "replay_kernel<ActBF16, 16, kModeFused, false>"
+KERNEL_NAME = "step_kernel<ActBF16, 16, true, false>"
 CPU_SAMPLE_SECONDS = 10.0
 CPU_MAX_CYCLES = 8
 

@@ -223,6 +223,61 @@ int fit_lds(gdnr::ReplayArgs* a, int es, bool stage_k, bool stage_v) {
               a->L, a->block_v, a->lds_bytes, kMaxLds);
 }
 
+// LDS plan of the step kernel (gdnr_step.hip, L <= kStepRing) for the
+// current gw / block_v: q | new k | k ring | flags | c_t | T0 | slot Gram per head |
+// v rows | flush: R | factors | K^T tiles | lam_all | U~/W tiles.
+int32_t layout_step(gdnr::ReplayArgs* a, int es) {
+  const int64_t K = gdnr::kKeyDim, LP = gdnr::kStepRing;
+  a->rpw = a->block_v;  // one streamer wave per head owns the head's block_v rows
+  a->sw = 2 * a->gw;     // plus one coefficient-chain wave per head
+  int64_t off = 0;
+  auto region = [&off](int32_t* field, int64_t bytes) {
+    *field = (int32_t)off;
+    off = align16(off + bytes);
+  };
+  region(&a->lds_q, K * es);
+  region(&a->lds_knew, K * es);
+  region(&a->lds_k, (int64_t)a->L * K * es);
+  region(&a->lds_flag, (int64_t)a->gw * 8);
+  region(&a->lds_c, (int64_t)a->gw * LP * 4);
+  region(&a->lds_t, (int64_t)a->gw * K * 4);
+  region(&a->lds_g, (int64_t)a->gw * (LP + 2) * (LP + 3) * 4);  // [slots, q, new k]^2, stride 19
+  region(&a->lds_v, (int64_t)a->gw * LP * a->rpw * es);
+  region(&a->lds_r, (int64_t)a->gw * LP * LP * 4);
+  region(&a->lds_fac, (int64_t)a->gw * LP * 16);
+  region(&a->lds_kt, K * LP * es);
+  region(&a->lds_lam, (int64_t)a->gw * 4);
+  region(&a->lds_u, (int64_t)a->gw * LP * 192);
+  a->lds_bytes = (int32_t)off;
+  return a->lds_bytes;
+}
+
+// value heads per workgroup and V-tile height for the step kernel: the
+// largest that fit in LDS with at most 8 waves, starting from the requested
+// block_v (results do not depend on either).
+int fit_step(gdnr::ReplayArgs* a, int es) {
+  const int32_t requested = a->block_v;
+  for (int bv = requested; bv >= 32; bv /= 2) {
+    if (a->V % bv) continue;
+    for (int gw = largest_group(a->G); gw >= 1; --gw) {
+      if (a->G % gw) continue;
+      a->gw = gw;
+      a->block_v = bv;
+      a->n_vt = a->V / bv;
+      if (layout_step(a, es) <= gdnr::kMaxStepLds && a->sw <= 8) return GDNR_OK;
+    }
+  }
+  return fail(GDNR_ERR_UNSUPPORTED, "no step-kernel tiling fits (V=%d, G=%d)", a->V, a->G);
+}
+
+// The step kernel forms per-lane ring / checkpoint offsets in 32 bits and
+// moves v-ring rows (and the new token's v) in pairs of elements.
+bool step_offsets_fit(const gdnr::ReplayArgs& a, int es) {
+  const int64_t lim = (int64_t)1 << 31;
+  const bool pairs = a.v_b % 2 == 0 && a.v_t % 2 == 0 && a.v_h % 2 == 0 && (a.mixed == nullptr || a.mx_b % 2 == 0);
+  return pairs && (int64_t)a.L * a.k_t * es < lim && (int64_t)a.L * a.v_t * es < lim && (int64_t)a.V * a.ck_v < lim;
+}
+
 int check_checkpoint(const gdnr_tensor* checkpoint, const gdnr_tensor* scale, const Geometry& g) {
   GDNR_TRY(check_desc(checkpoint, "checkpoint", 4));
   GDNR_TRY(check_dtype(checkpoint, "checkpoint", {GDNR_DTYPE_FP8E4M3FN, GDNR_DTYPE_U8}));
@@ -306,6 +361,11 @@ int launch_replay(const gdnr::ReplayArgs& a, int act, int mode, bool gate_f32, v
   if (act == GDNR_DTYPE_F16) return gdnr::launch_replay_f16(a, mode, gate_f32, stream);
   return gdnr::launch_replay_f32(a, mode, gate_f32, stream);
 }
+int launch_step(const gdnr::ReplayArgs& a, int act, bool fused, bool gate_f32, void* stream) {
+  if (act == GDNR_DTYPE_BF16) return gdnr::launch_step_bf16(a, fused, gate_f32, stream);
+  if (act == GDNR_DTYPE_F16) return gdnr::launch_step_f16(a, fused, gate_f32, stream);
+  return gdnr::launch_step_f32(a, fused, gate_f32, stream);
+}
 int launch_precompute(const gdnr::ReplayArgs& a, int act, void* stream) {
   if (act == GDNR_DTYPE_BF16) return gdnr::launch_precompute_bf16(a, stream);
   if (act == GDNR_DTYPE_F16) return gdnr::launch_precompute_f16(a, stream);
@@ -333,7 +393,7 @@ int check_prep_inputs(const gdnr_tensor* mixed_qkv, const gdnr_tensor* a, const 
     return fail(GDNR_ERR_INVALID_ARGUMENT, "mixed_qkv: shape [%lld, %lld], expected [%lld, >= %lld]",
                 (long long)mixed_qkv->shape[0], (long long)mixed_qkv->shape[1], (long long)g.B, (long long)width);
   GDNR_TRY(check_inner_unit(mixed_qkv, "mixed_qkv"));
-  GDNR_TRY(check_align(mixed_qkv, "mixed_qkv", 4));
+  GDNR_TRY(check_align(mixed_qkv, "mixed_qkv", 2 * elem_size(g.act)));
   GDNR_TRY(check_scalar_vec(a, "a", 2, {g.B, g.HV}));
   GDNR_TRY(check_scalar_vec(b, "b", 2, {g.B, g.HV}));
   if (a->dtype != b->dtype || (a->dtype != g.act && a->dtype != GDNR_DTYPE_F32))
@@ -449,6 +509,10 @@ int gdnr_replay_fp8(const gdnr_tensor* checkpoint, const gdnr_tensor* checkpoint
   a.out = out->data;
   a.o_b = out->strides[0];
   a.o_h = out->strides[1];
+  if (a.L <= gdnr::kStepRing && step_offsets_fit(a, elem_size(g.act))) {
+    GDNR_TRY(fit_step(&a, elem_size(g.act)));
+    return hip_status(launch_step(a, g.act, false, false, stream));
+  }
   GDNR_TRY(fit_lds(&a, elem_size(g.act), true, true));
   return hip_status(launch_replay(a, g.act, gdnr::kModeReplay, false, stream));
 }
@@ -525,7 +589,7 @@ int gdnr_prep_ring(const gdnr_tensor* mixed_qkv, const gdnr_tensor* a, const gdn
   g_last_error.clear();
   Geometry g;
   GDNR_TRY(check_ring(k_ring, v_ring, g_ring, beta_ring, &g, 4));
-  GDNR_TRY(check_act_tensor(q_out, "q_out", 3, {g.B, g.H, g.K}, g.act, 4));
+  GDNR_TRY(check_act_tensor(q_out, "q_out", 3, {g.B, g.H, g.K}, g.act, 2 * elem_size(g.act)));
   GDNR_TRY(check_prep_inputs(mixed_qkv, a, b, a_log, dt_bias, pos, g));
   if (g.B == 0) return GDNR_OK;
   gdnr::ReplayArgs r = {};
@@ -583,7 +647,7 @@ int gdnr_prep_replay_fp8(const gdnr_tensor* mixed_qkv, const gdnr_tensor* a, con
   Geometry g;
   GDNR_TRY(check_ring(k_ring, v_ring, g_ring, beta_ring, &g, 16));
   GDNR_TRY(check_checkpoint(checkpoint, checkpoint_scale, g));
-  GDNR_TRY(check_act_tensor(q_out, "q_out", 3, {g.B, g.H, g.K}, g.act, 4));
+  GDNR_TRY(check_act_tensor(q_out, "q_out", 3, {g.B, g.H, g.K}, g.act, 2 * elem_size(g.act)));
   GDNR_TRY(check_prep_inputs(mixed_qkv, a, b, a_log, dt_bias, pos, g));
   GDNR_TRY(check_index_vec(valid_len, "valid_len", g.B, false));
   GDNR_TRY(check_index_vec(flush, "flush", g.B, true));
@@ -603,6 +667,10 @@ int gdnr_prep_replay_fp8(const gdnr_tensor* mixed_qkv, const gdnr_tensor* a, con
   r.out = out->data;
   r.o_b = out->strides[0];
   r.o_h = out->strides[1];
+  if (r.L <= gdnr::kStepRing && step_offsets_fit(r, elem_size(g.act))) {
+    GDNR_TRY(fit_step(&r, elem_size(g.act)));
+    return hip_status(launch_step(r, g.act, true, a->dtype == GDNR_DTYPE_F32, stream));
+  }
   GDNR_TRY(fit_lds(&r, elem_size(g.act), true, true));
   return hip_status(launch_replay(r, g.act, gdnr::kModeFused, a->dtype == GDNR_DTYPE_F32, stream));
 }

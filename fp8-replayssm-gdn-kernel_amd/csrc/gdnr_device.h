@@ -14,11 +14,18 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 // ---------------------------------------------------------------- formats
 __device__ __forceinline__ float bf16_to_f32(uint32_t bits) { return __uint_as_float(bits << 16); }
 
-// float -> bfloat16 bits, round-to-nearest-even, NaN quietened (torch's rule).
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// float pair -> packed bfloat16 bits (lo in bits 0-15): one gfx950
+// v_cvt_pk_bf16_f32, round-to-nearest-even, NaN quietened -- torch's rule.
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  const f32x2_t v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+}
+// float -> bfloat16 bits (same conversion, one value).
 __device__ __forceinline__ uint32_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (u >> 16) | 0x40u;
-  return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+  return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)f);
 }
 
 // Storage traits of the activation dtype (q, k/v rings, out, mixed_qkv).
@@ -40,7 +47,7 @@ struct ActBF16 {
     uint32_t w = *(const uint32_t*)p;
     return make_float2(bf16_to_f32(w & 0xFFFFu), bf16_to_f32(w >> 16));
   }
-  __device__ static void st2(void* p, float x, float y) { *(uint32_t*)p = f32_to_bf16(x) | (f32_to_bf16(y) << 16); }
+  __device__ static void st2(void* p, float x, float y) { *(uint32_t*)p = pack_bf16x2(x, y); }
   // 16 consecutive elements at byte address p (16-byte aligned)
   __device__ static void ld16(const void* p, float* f) {
     const uint4* q = (const uint4*)p;

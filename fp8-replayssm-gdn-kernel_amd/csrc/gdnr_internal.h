@@ -52,7 +52,18 @@ struct ReplayArgs {
   float out_scale;             // K^-1/2
   // LDS byte offsets (computed on the host)
   int32_t lds_q, lds_k, lds_v, lds_gb, lds_t, lds_bytes;
+  // step kernel (gdnr_step.hip, rings of up to kStepRing tokens): waves per
+  // workgroup, V-rows per wave, the new token's k row, per-head publish
+  // flags, coefficients and [17 x 17] Gram matrices
+  int32_t sw, rpw, lds_knew, lds_flag, lds_c, lds_g;
+  // flush (MFMA rebuild), per head: R = (I + M)^-1 [16 x 16] f32, per-token
+  // factors (pre, post, dq, -) f32, lam_all f32; K^T operand tiles [K x 16]
+  // in the ring dtype; per wave U~^T and W^T operand tiles (3 KiB)
+  int32_t lds_r, lds_fac, lds_kt, lds_lam, lds_u;
 };
+
+constexpr int32_t kMaxStepLds = 160 * 1024;  // gfx950 LDS per workgroup
+constexpr int kStepRing = 16;                // ring capacity handled by the step kernel
 
 struct PrepArgs {
   const void* mixed; int64_t mx_b;
@@ -85,7 +96,8 @@ enum ReplayMode : int { kModeReplay = 0, kModeApply = 1, kModeFused = 2 };
 #define GDNR_DECLARE_LAUNCHERS(SUFFIX)                                                      \
   int launch_replay_##SUFFIX(const ReplayArgs& a, int mode, bool gate_f32, void* stream); \
   int launch_precompute_##SUFFIX(const ReplayArgs& a, void* stream);                      \
-  int launch_prep_##SUFFIX(const PrepArgs& a, bool gate_f32, void* stream);
+  int launch_prep_##SUFFIX(const PrepArgs& a, bool gate_f32, void* stream);                \
+  int launch_step_##SUFFIX(const ReplayArgs& a, bool fused, bool gate_f32, void* stream);
 GDNR_DECLARE_LAUNCHERS(bf16)
 GDNR_DECLARE_LAUNCHERS(f16)
 GDNR_DECLARE_LAUNCHERS(f32)

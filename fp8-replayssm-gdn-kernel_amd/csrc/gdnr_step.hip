@@ -1,0 +1,899 @@
+// gdnr_step.hip -- one ReplaySSM decode step on gfx950 (MI355X) for rings of
+// up to 16 tokens: replay or flush per sequence, optionally fused with the
+// full-contract preparation of the new token.
+//
+// Grid: x = V-tile + n_vt * (value-head group within the key head), y = key
+// head h, z = sequence b (no integer division on the way to the first load).
+// Workgroup = gw value heads sharing key head h, block_v V-rows of each, and
+// two waves per head:
+//   lead j (wave j): loads the k ring (all L slots; slots beyond the fill are
+//     read and ignored), q and the gates, prepares the new token (fused),
+//     forms the Gram matrix and the coefficient chain of head j, and
+//     publishes the coefficients through an LDS flag. It loads no checkpoint
+//     row: a wave whose loads back up in the memory pipeline cannot issue
+//     anything else, and the checkpoint stream would stall the chain.
+//   streamer j (wave gw + j): owns the block_v rows of head j -- v rows,
+//     vblock scales and NCH = block_v / 8 checkpoint loads of 16 bytes a lane
+//     in the MFMA operand layout (lane (l16, q4) of 16-row block i holds row
+//     l16, bytes [16 q4, +16) and [64 + 16 q4, +16)), which serves both the
+//     replay matvec and the flush rebuild. It starts streaming once its
+//     lead's ring has landed (so the ring requests of the grid reach memory
+//     first), waits for the coefficients, then emits its rows.
+//
+// Replay, the adjoint of the reference's reverse chain
+// (prototype/gdn_replayssm_fp8_kernel.py:121-173), in Gram form:
+//   dq_t = k_t.q, G_tu = k_t.k_u                   (MFMA Gram matrix of [K; q])
+//   s_t  = beta_t (dq_t - sum_{u>t} G_tu s_u)       (t descending)
+//   c_t  = s_t prod_{u>t} gamma_u,  T0 = prod_u gamma_u (q - sum_t s_t k_t)
+//   o    = ((scale * codes) . T0 + sum_t c_t v_t) K^-1/2
+// Flush: the forward rebuild in matrix form on MFMA (section 7), o from the
+// rebuilt state, requantisation in place.
+//
+// LDS: the k ring is stored with an XOR swizzle of 16-byte chunks (chunk c of
+// token t at position c ^ (t & 15)) so that operand reads of 16 different
+// tokens at one column hit 16 different bank groups. The new token's k lives
+// in a row of its own: the ring DMA of its slot may land after it is written.
+//
+// Compiled once per activation dtype (GDNR_ACT = 0 bf16, 1 f16, 2 f32).
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <type_traits>
+
+#include "gdnr_device.h"
+#include "gdnr_internal.h"
+
+#ifndef GDNR_ACT
+#error "compile with -DGDNR_ACT=0|1|2"
+#endif
+
+namespace gdnr {
+namespace {
+
+constexpr int K = kKeyDim;
+constexpr int LP = kStepRing;  // ring capacity of this kernel: one 16-token block
+
+typedef short bf16x4_t __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float readlane_fv(float x, int lane) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), lane));
+}
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+// Opaque copy: values derived from the result are recomputed inside the loop
+// that makes the copy instead of being hoisted out of it (and spilled).
+__device__ __forceinline__ uint32_t opaque(uint32_t x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+// 16-bit value at a wave-uniform address, through the scalar cache: the
+// aligned dword holding it (allocations are at least 4-byte granular).
+__device__ __forceinline__ uint32_t ld_u16_uniform(const uint16_t* p) {
+  const uintptr_t ad = (uintptr_t)p;
+  const uint32_t w = *(const uint32_t*)(ad & ~(uintptr_t)3);
+  return __builtin_amdgcn_readfirstlane((w >> (8u * (uint32_t)(ad & 2))) & 0xFFFFu);
+}
+// DPP move within a 16-lane row; lanes whose source is outside the row get `fill`.
+template <int CTRL>
+__device__ __forceinline__ float dpp_row(float x, float fill) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, fill), __builtin_bit_cast(int, x),
+                                                               CTRL, 0xF, 0xF, false));
+}
+// inclusive prefix / suffix products over the lanes of each 16-lane row
+__device__ __forceinline__ float row_prefix_prod(float x) {
+  x *= dpp_row<0x111>(x, 1.f);  // row_shr:1
+  x *= dpp_row<0x112>(x, 1.f);  // row_shr:2
+  x *= dpp_row<0x114>(x, 1.f);  // row_shr:4
+  x *= dpp_row<0x118>(x, 1.f);  // row_shr:8
+  return x;
+}
+__device__ __forceinline__ float row_suffix_prod(float x) {
+  x *= dpp_row<0x101>(x, 1.f);  // row_shl:1
+  x *= dpp_row<0x102>(x, 1.f);  // row_shl:2
+  x *= dpp_row<0x104>(x, 1.f);  // row_shl:4
+  x *= dpp_row<0x108>(x, 1.f);  // row_shl:8
+  return x;
+}
+
+// byte offset of byte `by` of token t's row in the swizzled k ring (ROWB = K * ES)
+template <int ROWB>
+__device__ __forceinline__ int kr_off(int t, int by) {
+  return t * ROWB + ((((by >> 4) ^ (t & 15))) << 4) + (by & 15);
+}
+
+// Rows of X = [k_0 .. k_{n-1}, q]: LDS byte address of byte `by` of row x
+// (x < n: the ring, or the new token's own row at x == pos; x >= n: q).
+// Rows beyond n are zeroed by the callers.
+struct XRows {
+  int lds_k, lds_knew, lds_q, n, pos;
+  template <int ROWB>
+  __device__ __forceinline__ int off(int x, int by) const {
+    return x < n ? (x == pos ? lds_knew + by : lds_k + kr_off<ROWB>(x, by)) : lds_q + by;
+  }
+};
+
+// One 16x16 tile of X_I X_J^T over K = 128 (rows ri, rj of this lane; rows
+// beyond n are zero). Result element e of lane l is D[4*(l/16) + e][l % 16].
+// bf16/f16: v_mfma_f32_16x16x32, lane l supplying row l % 16 and one 16-byte
+// chunk (8 columns) per instruction; the chunk order is the same for both
+// operands, which is all a Gram product needs.
+template <class Act>
+__device__ __forceinline__ f32x4_t gram_tile(const uint8_t* lds, const XRows& xr, int ri, int rj, int lane) {
+  constexpr int ROWB = K * Act::kBytes;
+  const int q4 = lane >> 4;
+  const bool zi = ri > xr.n, zj = rj > xr.n;
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+  if constexpr (std::is_same<Act, ActF32>::value) {
+#pragma unroll
+    for (int kc = 0; kc < K / 4; ++kc) {
+      float av = *(const float*)(lds + xr.off<ROWB>(ri, (kc * 4 + q4) * 4));
+      float bv = *(const float*)(lds + xr.off<ROWB>(rj, (kc * 4 + q4) * 4));
+      av = zi ? 0.f : av;
+      bv = zj ? 0.f : bv;
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc, 0, 0, 0);
+    }
+  } else {
+#pragma unroll
+    for (int m = 0; m < K / 32; ++m) {
+      uint4 av = *(const uint4*)(lds + xr.off<ROWB>(ri, (4 * m + q4) * 16));
+      uint4 bv = *(const uint4*)(lds + xr.off<ROWB>(rj, (4 * m + q4) * 16));
+      if (zi) av = make_uint4(0u, 0u, 0u, 0u);
+      if (zj) bv = make_uint4(0u, 0u, 0u, 0u);
+      if constexpr (std::is_same<Act, ActBF16>::value)
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, av), __builtin_bit_cast(bf16x8_t, bv),
+                                                      acc, 0, 0, 0);
+      else
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, av), __builtin_bit_cast(f16x8_t, bv),
+                                                     acc, 0, 0, 0);
+    }
+  }
+  return acc;
+}
+
+// The same tile over the slot rows Y = [ring slots 0..15, q, new k] (18 rows;
+// slots >= L, the new k when not fused and rows beyond 17 are zero), which
+// needs no per-sequence metadata: the chain later picks rows by (n, pos).
+template <class Act, bool FUSED>
+__device__ __forceinline__ f32x4_t gram_tile_slots(const uint8_t* lds, int lds_k, int lds_q, int lds_knew, int L, int ri,
+                                                   int rj, int lane) {
+  constexpr int ROWB = K * Act::kBytes;
+  const int q4 = lane >> 4;
+  auto row_off = [&](int x, int by) { return x < 16 ? lds_k + kr_off<ROWB>(x, by) : (x == 16 ? lds_q : lds_knew) + by; };
+  auto zero_row = [&](int x) { return x < 16 ? x >= L : (x == 17 ? !FUSED : x > 17); };
+  const bool zi = zero_row(ri), zj = zero_row(rj);
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+  if constexpr (std::is_same<Act, ActF32>::value) {
+#pragma unroll
+    for (int kc = 0; kc < K / 4; ++kc) {
+      float av = *(const float*)(lds + row_off(ri, (kc * 4 + q4) * 4));
+      float bv = *(const float*)(lds + row_off(rj, (kc * 4 + q4) * 4));
+      av = zi ? 0.f : av;
+      bv = zj ? 0.f : bv;
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc, 0, 0, 0);
+    }
+  } else {
+#pragma unroll
+    for (int m = 0; m < K / 32; ++m) {
+      uint4 av = *(const uint4*)(lds + row_off(ri, (4 * m + q4) * 16));
+      uint4 bv = *(const uint4*)(lds + row_off(rj, (4 * m + q4) * 16));
+      if (zi) av = make_uint4(0u, 0u, 0u, 0u);
+      if (zj) bv = make_uint4(0u, 0u, 0u, 0u);
+      if constexpr (std::is_same<Act, ActBF16>::value)
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, av), __builtin_bit_cast(bf16x8_t, bv),
+                                                      acc, 0, 0, 0);
+      else
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, av), __builtin_bit_cast(f16x8_t, bv),
+                                                     acc, 0, 0, 0);
+    }
+  }
+  return acc;
+}
+
+template <bool GATE_F32, class Act>
+__device__ __forceinline__ float ld_gate(const void* p, int64_t i) {
+  if constexpr (GATE_F32) return ((const float*)p)[i];
+  else return Act::ld(p, i);
+}
+
+template <class Act, int NCH, bool FUSED, bool GATE_F32>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void step_kernel(const ReplayArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  constexpr int ES = Act::kBytes;
+  constexpr int ROWB = K * ES;          // bytes of one k-ring row
+  constexpr int RPW = 8 * NCH;          // V-rows per streamer (= block_v)
+  constexpr int NBLK = NCH / 2;         // 16-row blocks per wave
+  constexpr int NVB = NCH / 4;          // 32-row vblocks per wave
+  constexpr int CPT_K = ROWB / 16;      // 16-byte chunks per key row
+  constexpr int CPT_V = RPW * ES / 16;  // 16-byte chunks of one token's slice of this wave's v rows
+  constexpr bool BF16 = std::is_same<Act, ActBF16>::value;
+  constexpr bool F16 = std::is_same<Act, ActF16>::value;
+
+  const int lane = threadIdx.x & 63;
+  const int q4 = lane >> 4, l16 = lane & 15;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nw = a.sw;
+  int vt = 0, sub = blockIdx.x;
+  if (a.n_vt > 1) {
+    sub = blockIdx.x / a.n_vt;
+    vt = blockIdx.x - sub * a.n_vt;
+  }
+  const int h = blockIdx.y, b = blockIdx.z;
+  const int hv0 = h * a.G + sub * a.gw;
+  const bool head_lead = wave < a.gw;                  // waves [0, gw): coefficient chains
+  const int j_head = head_lead ? wave : wave - a.gw;  // waves [gw, 2 gw): the rows of head j
+  constexpr int r0 = 0;
+  const int hv = hv0 + j_head;
+  const int v0 = vt * a.block_v;
+  const int L = a.L;
+
+  // ---- 0. the head leads publish their coefficients through LDS flags -------------
+  // flags[j]: head j's coefficients are in LDS; flags[gw + j]: its ring has landed
+  int* flags = (int*)(lds + a.lds_flag);
+  if (wave == 0 && lane < 2 * a.gw) flags[lane] = 0;
+  GDNR_WAIT_LGKM0();
+  __builtin_amdgcn_s_barrier();  // B0, the only workgroup barrier
+
+  // ---- 1. metadata (scalar), then the loads of this wave's role ------------------
+  const int n_raw = a.valid_len[(int64_t)b * a.vl_s];
+  int pos_raw = -1;
+  if constexpr (FUSED) pos_raw = a.pos[(int64_t)b * a.pos_s];
+  // flush flag: the aligned dword holding the byte (allocations are at least
+  // 4-byte granular, so it stays in bounds)
+  uint32_t flush_word = 0, flush_shift = 0;
+  if (a.flush) {
+    const uintptr_t fa = (uintptr_t)(a.flush + (int64_t)b * a.fl_s);
+    flush_word = *(const uint32_t*)(fa & ~(uintptr_t)3);
+    flush_shift = 8u * (uint32_t)(fa & 3);
+  }
+  // per-sequence metadata, read once the wave needs it
+  int n = 0, pos = -1;
+  bool do_flush = false;
+  auto read_meta = [&]() {
+    GDNR_WAIT_LGKM0();
+    n = __builtin_amdgcn_readfirstlane(n_raw);
+    n = n < 0 ? 0 : (n > L ? L : n);
+    if constexpr (FUSED) {
+      const int p = __builtin_amdgcn_readfirstlane(pos_raw);
+      pos = (p >= 0 && p < L) ? p : -1;
+    }
+    do_flush = __builtin_amdgcn_readfirstlane((flush_word >> flush_shift) & 0xFFu) != 0;
+  };
+
+  // ---- 2-4. head lead: new token, Gram, coefficient chain, publish ---------------
+  // The lead loads what the chain needs -- the k ring (all L slots; each lead
+  // loads the whole ring: the second copy lands on identical bytes and hits
+  // in L2), q, the gates of its head -- and raises flags[gw + j] when they
+  // have landed, which starts its streamer: the ring requests of the grid
+  // reach memory ahead of the checkpoint stream.
+  if (head_lead) {
+    const int j = j_head;
+    typename Act::Pair q_bits{}, k_bits{};
+    float a_raw = 0.f, b_raw = 0.f, alog_raw = 0.f, dtb_raw = 0.f;
+    typename Act::Bits g_bits = 0, b_bits = 0;
+    float q0 = 0.f, q1 = 0.f, k0 = 0.f, k1 = 0.f, gate_new = 0.f, beta_new = 0.f;
+    // loads of the chain (the metadata may still be in flight)
+    const uint8_t* kbase = (const uint8_t*)a.k + ((int64_t)b * a.k_b + (int64_t)h * a.k_h) * ES;
+    const uint32_t kt_bytes = (uint32_t)(a.k_t * ES);
+    // destination chunk p of token t holds source chunk p ^ (t & 15)
+    for (int c0 = 0; c0 < L * CPT_K; c0 += 64) {
+      const int c = c0 + lane;
+      const int t = c / CPT_K, ch = c % CPT_K;
+      if (c < L * CPT_K)
+        __builtin_amdgcn_global_load_lds(kbase + (uint32_t)(t * kt_bytes + 16 * (ch ^ (t & 15))),
+                                         (lds_void_t*)(lds + a.lds_k + c0 * 16), 16, 0, 0);
+    }
+    if constexpr (!FUSED) {
+      if (lane < CPT_K) {
+        const uint8_t* qrow = (const uint8_t*)a.q + ((int64_t)b * a.q_b + (int64_t)h * a.q_h) * ES;
+        __builtin_amdgcn_global_load_lds(qrow + 16 * lane, (lds_void_t*)(lds + a.lds_q), 16, 0, 0);
+      }
+    } else {
+      const uint8_t* row = (const uint8_t*)a.mixed + (int64_t)b * a.mx_b * ES;
+      q_bits = Act::ld_pair_bits(row + (h * K + 2 * lane) * ES);
+      k_bits = Act::ld_pair_bits(row + (a.H * K + h * K + 2 * lane) * ES);
+      if (lane == 0) {
+        a_raw = ld_gate<GATE_F32, Act>(a.a, (int64_t)b * a.a_b + (int64_t)hv * a.a_h);
+        b_raw = ld_gate<GATE_F32, Act>(a.bgate, (int64_t)b * a.bg_b + (int64_t)hv * a.bg_h);
+        alog_raw = a.a_log[(int64_t)hv * a.al_s];
+        dtb_raw = a.dt_bias[(int64_t)hv * a.db_s];
+      }
+    }
+    if (lane < L) {
+      g_bits = Act::ld_bits(a.g, (int64_t)b * a.g_b + (int64_t)lane * a.g_t + (int64_t)hv * a.g_h);
+      b_bits = Act::ld_bits(a.beta, (int64_t)b * a.be_b + (int64_t)lane * a.be_t + (int64_t)hv * a.be_h);
+    }
+    GDNR_WAIT_VMCNT(0);  // ring landed; the metadata may still be in flight
+    __hip_atomic_store(flags + a.gw + j, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if constexpr (FUSED) {
+      // full-contract preparation of the new token's q and k (reference
+      // kernel:504-533); every lead writes the same values
+      const float2 qr = Act::from_pair(q_bits), kr = Act::from_pair(k_bits);
+      const float qd = sqrtf(wave_sum(fmaf(qr.y, qr.y, qr.x * qr.x)) + 1e-6f);
+      const float kd = sqrtf(wave_sum(fmaf(kr.y, kr.y, kr.x * kr.x)) + 1e-6f);
+      q0 = Act::round(qr.x / qd);
+      q1 = Act::round(qr.y / qd);
+      k0 = Act::round(kr.x / kd);
+      k1 = Act::round(kr.y / kd);
+      Act::st2(lds + a.lds_q + 2 * lane * ES, q0, q1);
+      Act::st2(lds + a.lds_knew + 2 * lane * ES, k0, k1);
+    }
+    // gates (gamma = e^g, beta) of the ring slots
+    float2 gb = make_float2(1.f, 0.f);
+    if (lane < L) gb = make_float2(expf(Act::from_bits(g_bits)), Act::from_bits(b_bits));
+    if constexpr (FUSED) {
+      // gates of the new token (reference kernel:534-562)
+      float gn = 0.f, bn = 0.f;
+      if (lane == 0) {
+        const float x = a_raw + dtb_raw;
+        const float sp = x <= 20.0f ? logf(1.0f + expf(x)) : x;  // kernel:560, as written there
+        gn = Act::round(-expf(alog_raw) * sp);
+        bn = Act::round(1.0f / (1.0f + expf(-b_raw)));
+      }
+      gate_new = readlane_fv(gn, 0);
+      beta_new = readlane_fv(bn, 0);
+    }
+    // Gram of the slot rows Y = [slots 0..15, q, new k]: tiles (0,0), (0,1),
+    // (1,1), of which rows / columns 0..17 are kept ([18 x 18], stride 19)
+    float* G = (float*)(lds + a.lds_g) + j * 18 * 19;
+#pragma unroll 1
+    for (int idx = 0; idx < 3; ++idx) {
+      const int ti = idx == 2 ? 1 : 0, tj = idx == 0 ? 0 : 1;
+      const int ri = ti * 16 + l16, rj = tj * 16 + l16;
+      const f32x4_t d = gram_tile_slots<Act, FUSED>(lds, a.lds_k, a.lds_q, a.lds_knew, L, ri, rj, lane);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int r = ti * 16 + 4 * q4 + e;
+        if (r < 18 && rj < 18) {
+          G[r * 19 + rj] = d[e];
+          G[rj * 19 + r] = d[e];
+        }
+      }
+    }
+    read_meta();
+    const XRows xr{a.lds_k, a.lds_knew, a.lds_q, n, pos};
+    // token t < n is slot t, except the new token (row 17) at t == pos; q is row 16
+    const bool on = lane < n;
+    if (FUSED && lane == pos) gb = make_float2(expf(gate_new), beta_new);
+    if (!on) gb = make_float2(1.f, 0.f);
+    const int my_row = lane == pos ? 17 : l16;
+    if (do_flush) {
+      // K^T as MFMA A-operand tiles of 16 K-columns x 16 tokens, tile ct at
+      // ct * 256 * ES bytes; row r of tile ct is K column
+      // 64 (ct / 4) + 16 (r / 4) + 4 (ct % 4) + r % 4, the column order of the
+      // checkpoint operand in section 7. Raw ring bits, zero for tokens t >= n;
+      // every lead writes the same tiles.
+#pragma unroll
+      for (int cc = 0; cc < K / 64; ++cc) {
+        const int c = cc * 64 + lane;
+        const int ct = 4 * (c >> 6) + ((c >> 2) & 3);
+        const int row = 4 * ((c >> 4) & 3) + (c & 3);
+        uint32_t wd[4 * ES];  // 16 tokens x ES bytes
+        if constexpr (ES == 2) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const int t0 = 2 * i, t1 = t0 + 1;
+            const uint32_t lo = *(const uint16_t*)(lds + xr.off<ROWB>(t0, c * 2));
+            const uint32_t hi = *(const uint16_t*)(lds + xr.off<ROWB>(t1, c * 2));
+            wd[i] = (t0 < n ? lo : 0u) | (t1 < n ? hi << 16 : 0u);
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const uint32_t x = *(const uint32_t*)(lds + xr.off<ROWB>(i, c * 4));
+            wd[i] = i < n ? x : 0u;
+          }
+        }
+        uint4* dst = (uint4*)(lds + a.lds_kt + ct * 256 * ES + row * 16 * ES);
+#pragma unroll
+        for (int i = 0; i < ES; ++i) dst[i] = make_uint4(wd[4 * i], wd[4 * i + 1], wd[4 * i + 2], wd[4 * i + 3]);
+      }
+    }
+    const float dq = on ? G[my_row * 19 + 16] : 0.f;
+    // prod_{x >= t} gamma_x (inclusive suffix) and prod_{x > t} gamma_x
+    const float suf_in = row_suffix_prod(gb.x);
+    const float suf_ex = dpp_row<0x101>(suf_in, 1.f);
+    const float lam_all = readlane_fv(suf_in, 0);
+    if (!do_flush) {
+      // s_t, t descending: acc_l = sum_{u > t} G[l][u] s_u
+      float gcol[LP];
+#pragma unroll
+      for (int i = 0; i < LP; ++i) gcol[i] = G[my_row * 19 + (i == pos ? 17 : i)];
+      float acc = 0.f, s_mine = 0.f;
+      const float beta = gb.y;
+#pragma unroll
+      for (int t = LP - 1; t >= 0; --t) {
+        if (t < n) {
+          const float sv = readlane_fv(beta * (dq - acc), t);
+          s_mine = lane == t ? sv : s_mine;
+          acc = fmaf(gcol[t], sv, acc);
+        }
+      }
+      if (lane < LP) ((float*)(lds + a.lds_c))[j * LP + lane] = on ? s_mine * suf_ex : 0.f;
+      // T0 = lam_all (q - sum_t s_t k_t), lane owns columns 2 lane, 2 lane + 1
+      float2 kk[LP];
+#pragma unroll
+      for (int t = 0; t < LP; ++t) kk[t] = Act::ld2(lds + xr.off<ROWB>(t, 2 * lane * ES));
+      float2 U = Act::ld2(lds + a.lds_q + 2 * lane * ES);
+#pragma unroll
+      for (int t = 0; t < LP; ++t) {
+        if (t < n) {
+          const float st = readlane_fv(s_mine, t);
+          U.x = fmaf(-st, kk[t].x, U.x);
+          U.y = fmaf(-st, kk[t].y, U.y);
+        }
+      }
+      *(float2*)(lds + a.lds_t + (j * K + 2 * lane) * 4) = make_float2(lam_all * U.x, lam_all * U.y);
+    } else {
+      // flush factors of head j:
+      //   pre_t  = prod_{x<=t} gamma_x        post_t = beta_t prod_{x>t} gamma_x
+      //   M[t][s] = beta_s prod_{s<x<=t} gamma_x (k_s . k_t)   (s < t)
+      // so that the forward residuals u_t = v_t - (gamma_t S_t) k_t obey
+      //   u_t = (v_t - pre_t S_0 k_t) - sum_{s<t} M[t][s] u_s,  i.e.  u = R w, R = (I + M)^-1.
+      const float pre = row_prefix_prod(gb.x);
+      const float post = gb.y * suf_ex;
+      if (lane < LP)
+        ((float4*)(lds + a.lds_fac))[j * LP + lane] = make_float4(on ? pre : 0.f, on ? post : 0.f, dq, 0.f);
+      if (lane == 0) ((float*)(lds + a.lds_lam))[j] = lam_all;
+      // M column s = lane and R column c = lane in registers; R by forward
+      // substitution (I + M) R = I down the rows
+      float mc[LP];
+      float run = 1.f;
+#pragma unroll
+      for (int t = 0; t < LP; ++t) {
+        const float gt = readlane_fv(gb.x, t);
+        if (t > lane) run *= gt;
+        mc[t] = (lane < t && t < n) ? gb.y * run * G[my_row * 19 + (t == pos ? 17 : t)] : 0.f;
+      }
+      float r[LP];
+#pragma unroll
+      for (int t = 0; t < LP; ++t) {
+        float x = (t == lane) ? 1.f : 0.f;
+#pragma unroll
+        for (int s2 = 0; s2 < t; ++s2) x = fmaf(-readlane_fv(mc[t], s2), r[s2], x);
+        r[t] = x;
+      }
+      if (lane < LP) {
+        float* Rj = (float*)(lds + a.lds_r) + j * LP * LP;
+#pragma unroll
+        for (int t = 0; t < LP; ++t) Rj[t * LP + lane] = (t < n && on) ? r[t] : 0.f;
+      }
+    }
+    // publish: this head's coefficients (and the shared q / new k / K^T) are in LDS
+    __hip_atomic_store(flags + j, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if constexpr (FUSED) {
+      // ring append of the new token's q (output), k and gates
+      if (j == 0 && vt == 0 && sub == 0) {
+        uint8_t* qo = (uint8_t*)a.q_out + ((int64_t)b * a.qo_b + (int64_t)h * a.qo_h) * ES;
+        Act::st2(qo + 2 * lane * ES, q0, q1);
+        if (pos >= 0) {
+          uint8_t* kr_out = (uint8_t*)a.k + ((int64_t)b * a.k_b + (int64_t)pos * a.k_t + (int64_t)h * a.k_h) * ES;
+          Act::st2(kr_out + 2 * lane * ES, k0, k1);
+        }
+      }
+      if (vt == 0 && pos >= 0 && lane == 0) {
+        Act::st(a.g, (int64_t)b * a.g_b + (int64_t)pos * a.g_t + (int64_t)hv * a.g_h, gate_new);
+        Act::st(a.beta, (int64_t)b * a.be_b + (int64_t)pos * a.be_t + (int64_t)hv * a.be_h, beta_new);
+      }
+    }
+    return;
+  }
+  // ---- streamer of head j_head ---------------------------------------------------
+  // this wave's rows: v rows (all L slots) -> LDS, the new v (fused), the
+  // vblock scales, then (replay) the checkpoint rows: ck[hh * NBLK + i] = row
+  // 16 i + l16, bytes [64 hh + 16 q4, +16); word w of it holds columns
+  // 64 hh + 16 q4 + 4 w + e
+  uint8_t* vbuf = lds + a.lds_v + j_head * LP * RPW * ES;
+  uint16_t* scale_hv = a.scale + (int64_t)b * a.sc_b + (int64_t)hv * a.sc_h;
+  uint8_t* ck_rows = a.ckpt + (int64_t)b * a.ck_b + (int64_t)hv * a.ck_h + (int64_t)(v0 + r0) * a.ck_v;
+  typename Act::Pair vnew_bits{};  // rows 2 lane, 2 lane + 1 of the new v
+  uint32_t sc_bits[NVB];  // scalar
+  uint4 ck[NCH];
+  auto issue_rows = [&]() {
+    const uint8_t* vbase = (const uint8_t*)a.v + ((int64_t)b * a.v_b + (int64_t)hv * a.v_h + v0 + r0) * ES;
+    const uint32_t vt_bytes = (uint32_t)(a.v_t * ES);
+    for (int c0 = 0; c0 < L * CPT_V; c0 += 64) {
+      const int c = c0 + lane;
+      const int t = c / CPT_V, ch = c % CPT_V;
+      if (c < L * CPT_V)
+        __builtin_amdgcn_global_load_lds(vbase + (uint32_t)(t * vt_bytes + 16 * ch), (lds_void_t*)(vbuf + c0 * 16), 16,
+                                         0, 0);
+    }
+    if constexpr (FUSED) {
+      if (lane < RPW / 2)
+        vnew_bits = Act::ld_pair_bits((const uint8_t*)a.mixed +
+                                      ((int64_t)b * a.mx_b + 2 * a.H * K + hv * a.V + v0 + r0 + 2 * lane) * ES);
+    }
+#pragma unroll
+    for (int p = 0; p < NVB; ++p) sc_bits[p] = ld_u16_uniform(scale_hv + (int64_t)((v0 + r0) / kVBlock + p) * a.sc_v);
+  };
+  // checkpoint rows at a uniform base per 16-row block + one 32-bit lane offset
+  const uint32_t ck_lo = (uint32_t)l16 * (uint32_t)a.ck_v + 16 * q4;
+  auto issue_ck = [&]() {
+    GDNR_COMPILER_FENCE();
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+      for (int i = 0; i < NBLK; ++i) {
+        const uint8_t* base = ck_rows + (int64_t)(16 * i) * a.ck_v + 64 * hh;
+        ck[hh * NBLK + i] = *(const uint4*)(base + ck_lo);
+      }
+    GDNR_COMPILER_FENCE();
+  };
+  // stream once the lead's ring has landed (bounded wait: the lead always raises the flag)
+  for (int it = 0; it < (1 << 22); ++it) {
+    if (__hip_atomic_load(flags + a.gw + j_head, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != 0) break;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  // The metadata (requested at kernel start) decides the load plan: a replay
+  // requests all of its checkpoint rows now, a flush one vblock at a time in
+  // section 7 (its registers go to the rebuild instead).
+  read_meta();
+  issue_rows();
+  // ================= all waves: own rows =======================================
+  const int64_t out_base = (int64_t)b * a.o_b + (int64_t)hv * a.o_h + v0 + r0;
+  // ring append of the new token's v rows (full contract): issued last, after every load
+  auto append_token = [&]() {
+    if constexpr (FUSED) {
+      if (pos >= 0 && lane < RPW / 2) {
+        const float2 vn = Act::from_pair(vnew_bits);
+        Act::st2((uint8_t*)a.v + ((int64_t)b * a.v_b + (int64_t)pos * a.v_t + (int64_t)hv * a.v_h + v0 + r0 + 2 * lane) * ES,
+                 vn.x, vn.y);
+      }
+    }
+  };
+
+  // the new v into this head's rows, then wait for the lead's coefficients
+  auto await_coefficients = [&]() {
+    if constexpr (FUSED) {
+      if (pos >= 0 && lane < RPW / 2) {
+        const float2 vn = Act::from_pair(vnew_bits);
+        Act::st2(vbuf + (pos * RPW + 2 * lane) * ES, vn.x, vn.y);
+      }
+    }
+    // wait for this head's lead (bounded: the lead always publishes)
+    for (int it = 0; it < (1 << 22); ++it) {
+      if (__hip_atomic_load(flags + j_head, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) != 0) break;
+      __builtin_amdgcn_s_sleep(1);
+    }
+  };
+  const XRows xr{a.lds_k, a.lds_knew, a.lds_q, n, pos};
+
+  // The replay and flush tails share no code after this point (each returns),
+  // so the checkpoint registers of the replay never meet the registers of the
+  // rebuild.
+  if (!do_flush) {
+    // ---- replay: o = (scale * codes) . T0 + sum_t c_t v_t -------------------
+    issue_ck();
+    GDNR_WAIT_VMCNT(NCH);  // own v rows, new v and scales landed; checkpoint rows still streaming
+    await_coefficients();
+    // lane (l16, q4) holds, per block i, row 16 i + l16 at columns
+    // 64 hh + 16 q4 + [0, 16): partial dots, then a 4-lane butterfly over q4
+    // one half (hh) of the columns at a time: 16 values of T0 in registers
+    float P[NBLK];
+#pragma unroll
+    for (int i = 0; i < NBLK; ++i) P[i] = 0.f;
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      float Tv[16];
+      const float4* tp = (const float4*)(lds + a.lds_t + (j_head * K + 64 * hh + 16 * q4) * 4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float4 w = tp[i];
+        Tv[4 * i] = w.x;
+        Tv[4 * i + 1] = w.y;
+        Tv[4 * i + 2] = w.z;
+        Tv[4 * i + 3] = w.w;
+      }
+#pragma unroll
+      for (int i = 0; i < NBLK; ++i) {
+        const uint4 c = ck[hh * NBLK + i];
+        const uint32_t w4[4] = {c.x, c.y, c.z, c.w};
+        float p = P[i];
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          float f[4];
+          fp8x4_to_f32(w4[w], f);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) p = fmaf(f[e], Tv[4 * w + e], p);
+        }
+        P[i] = p;
+      }
+    }
+    // butterfly over q4 (lanes l16 + 16 q4): step 1 (xor 16) keeps the blocks
+    // with i % 2 == q4 % 2, step 2 (xor 32) those with (i / 2) % 2 == q4 / 2, so
+    // lane l ends with the totals of rows 64 m + l (NBLK >= 4), or lanes q4 and
+    // q4 ^ 2 both with row 16 (q4 % 2) + l16 (NBLK = 2)
+    const bool hi1 = (q4 & 1) != 0, hi2 = (q4 & 2) != 0;
+    float R2[NBLK / 2];
+#pragma unroll
+    for (int m = 0; m < NBLK / 2; ++m) {
+      const float send = hi1 ? P[2 * m] : P[2 * m + 1];
+      const float keep = hi1 ? P[2 * m + 1] : P[2 * m];
+      R2[m] = keep + __shfl_xor(send, 16);
+    }
+    constexpr int NOUT = NBLK >= 4 ? NBLK / 4 : 1;
+    float tot[NOUT];
+    int rows[NOUT];
+    if constexpr (NBLK >= 4) {
+#pragma unroll
+      for (int m = 0; m < NOUT; ++m) {
+        const float send = hi2 ? R2[2 * m] : R2[2 * m + 1];
+        const float keep = hi2 ? R2[2 * m + 1] : R2[2 * m];
+        tot[m] = keep + __shfl_xor(send, 32);
+        rows[m] = 64 * m + lane;
+      }
+    } else {
+      tot[0] = R2[0] + __shfl_xor(R2[0], 32);
+      rows[0] = 16 * (q4 & 1) + l16;
+    }
+    const float* cj = (const float*)(lds + a.lds_c) + j_head * LP;
+#pragma unroll
+    for (int m = 0; m < NOUT; ++m) {
+      const int row = rows[m];  // row within this head's block_v rows
+      float acc = 0.f;
+#pragma unroll
+      for (int t = 0; t < LP; ++t) {
+        if (t < n) acc = fmaf(readlane_fv(cj[t], 0), Act::ld(vbuf, t * RPW + row), acc);
+      }
+      const float sc = f16_bits_to_f32((uint16_t)sc_bits[NVB > 1 ? (row >> 5) : 0]);
+      if (NBLK >= 4 || q4 < 2) Act::st(a.out, out_base + row, fmaf(tot[m], sc, acc) * a.out_scale);
+    }
+    append_token();
+    return;
+  }
+
+  // ---- 7. flush: MFMA rebuild of this wave's rows, emit, requantise in place
+  GDNR_WAIT_VMCNT(0);
+  await_coefficients();
+  // Per vblock p (32 rows = 16-row blocks 2p, 2p + 1) lane l owns row l % 16
+  // of a block; the contraction walks the columns in the order of ck, so every
+  // checkpoint operand comes straight from those registers and the
+  // requantised codes go back as the same two 16-byte words.
+  //   A.  P^T = [K; q] S_0^T          (tokens x rows; the q row gives S_0 q)
+  //       W^T = v - pre . P^T
+  //   B.  U^T = R W^T,  U~^T = post . U^T,  o = lam_all S_0 q + sum_t U~^T[t] (k_t . q)
+  //   C.  S_n^T = lam_all S_0^T + K^T U~^T, two passes over the vblock:
+  //       amax, then requantisation.
+  // W^T and U~^T tiles are parked in this wave's LDS area in the MFMA
+  // B-operand layout ([tile][lane], 16 bytes a lane).
+  {
+    const int ntbx = n < LP ? 1 : 2;  // token blocks including the q row at index n
+    const float* Rj = (const float*)(lds + a.lds_r) + j_head * LP * LP;
+    const float4* fac = (const float4*)(lds + a.lds_fac) + j_head * LP;
+    const float lam_all = ((const float*)(lds + a.lds_lam))[j_head];
+    uint4* ubuf = (uint4*)(lds + a.lds_u + j_head * LP * 192);  // U~^T: [block mm][lane]
+    float4* wbuf = (float4*)(ubuf + 2 * 64);                   // W^T:  [lane]
+    // codes of vblock p: cf[hh * 2 + mm] (the layout of ck), next vblock prefetched
+    uint4 cf[4], cn[4];
+    auto load_vb = [&](int p, uint4* d) {
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+        for (int mm = 0; mm < 2; ++mm)
+          d[hh * 2 + mm] = *(const uint4*)(ck_rows + (int64_t)(32 * p + 16 * mm) * a.ck_v + 64 * hh + ck_lo);
+    };
+    load_vb(0, cf);
+#pragma unroll 1
+    for (int p = 0; p < NVB; ++p) {
+      if (p + 1 < NVB) load_vb(p + 1, cn);
+      const float sc = f16_bits_to_f32((uint16_t)ld_u16_uniform(scale_hv + (int64_t)((v0 + r0) / kVBlock + p) * a.sc_v));
+#pragma unroll
+      for (int mm = 0; mm < 2; ++mm) {
+        const int blk = 2 * p + mm;
+        const int rl = 16 * blk + l16;  // row within this wave's rows
+        const uint4 c0 = cf[mm], c1 = cf[2 + mm];
+        const uint32_t cw[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+        float o_part = 0.f;
+        // A: P^T blocks and W^T
+#pragma unroll 1
+        for (int tb = 0; tb < ntbx; ++tb) {
+          const int x = tb * 16 + l16;  // token row of X supplied by this lane
+          const bool zero_x = x > n;
+          f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+          if constexpr (BF16 || F16) {
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+              // columns 64 (m / 2) + 16 q4 + 8 (m % 2) + [0, 8): words 2m, 2m + 1
+              uint4 av = *(const uint4*)(lds + xr.off<ROWB>(x, (64 * (m >> 1) + 16 * q4 + 8 * (m & 1)) * 2));
+              if (zero_x) av = make_uint4(0u, 0u, 0u, 0u);
+              float f[8];
+              fp8x4_to_f32(opaque(cw[2 * m]), f);
+              fp8x4_to_f32(opaque(cw[2 * m + 1]), f + 4);
+              if constexpr (BF16) {
+                // e4m3 values are exact in bf16
+                const uint4 bv = make_uint4(pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]), pack_bf16x2(f[4], f[5]),
+                                            pack_bf16x2(f[6], f[7]));
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, av),
+                                                              __builtin_bit_cast(bf16x8_t, bv), acc, 0, 0, 0);
+              } else {
+                const f16x8_t bv = {(_Float16)f[0], (_Float16)f[1], (_Float16)f[2], (_Float16)f[3],
+                                    (_Float16)f[4], (_Float16)f[5], (_Float16)f[6], (_Float16)f[7]};
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, av), bv, acc, 0, 0, 0);
+              }
+            }
+          } else {
+#pragma unroll
+            for (int kc = 0; kc < 8; ++kc) {
+              const int col = 64 * (kc >> 2) + 16 * q4 + 4 * (kc & 3);
+              float f[4];
+              fp8x4_to_f32(opaque(cw[kc]), f);
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                float av = *(const float*)(lds + xr.off<ROWB>(x, (col + e) * 4));
+                av = zero_x ? 0.f : av;
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av, f[e], acc, 0, 0, 0);
+              }
+            }
+          }
+          float wv[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int t = tb * 16 + 4 * q4 + e;
+            const float pv = acc[e] * sc;
+            if (t < n) {
+              wv[e] = Act::ld(vbuf, t * RPW + rl) - fac[t].x * pv;
+            } else {
+              wv[e] = 0.f;
+              if (t == n) o_part = fmaf(lam_all, pv, o_part);
+            }
+          }
+          // the block holding only the q row (tb == 1) is not a token block of W^T
+          if (tb == 0) wbuf[lane] = make_float4(wv[0], wv[1], wv[2], wv[3]);
+        }
+        // B: U^T = R W^T (fp32 MFMA, contraction index q4 <-> token 4 q4 + e)
+        {
+          f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+          const float4 wv = wbuf[lane];
+          const float* rrow = Rj + l16 * LP + 4 * q4;
+          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(rrow[0], wv.x, acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(rrow[1], wv.y, acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(rrow[2], wv.z, acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(rrow[3], wv.w, acc, 0, 0, 0);
+          float ut[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float4 f = fac[4 * q4 + e];
+            ut[e] = acc[e] * f.y;
+            o_part = fmaf(ut[e], f.z, o_part);
+          }
+          uint4 packed;
+          if constexpr (BF16) {
+            // hi/lo split: U~ = hi + lo to ~16 bits, both halves bf16 MFMA operands
+            const uint32_t h01 = pack_bf16x2(ut[0], ut[1]), h23 = pack_bf16x2(ut[2], ut[3]);
+            const uint32_t l01 =
+                pack_bf16x2(ut[0] - __uint_as_float(h01 << 16), ut[1] - __uint_as_float(h01 & 0xFFFF0000u));
+            const uint32_t l23 =
+                pack_bf16x2(ut[2] - __uint_as_float(h23 << 16), ut[3] - __uint_as_float(h23 & 0xFFFF0000u));
+            packed = make_uint4(h01, h23, l01, l23);
+          } else {
+            packed = make_uint4(__float_as_uint(ut[0]), __float_as_uint(ut[1]), __float_as_uint(ut[2]),
+                                __float_as_uint(ut[3]));
+          }
+          ubuf[mm * 64 + lane] = packed;
+        }
+        o_part += __shfl_xor(o_part, 16);
+        o_part += __shfl_xor(o_part, 32);
+        if (q4 == 0) Act::st(a.out, out_base + rl, o_part * a.out_scale);
+      }
+      // C: S_n^T tiles sn[ct] of block mm (ct = 4 hh + w): D row 4 q4 + e of
+      // tile ct is column 64 hh + 16 q4 + 4 w + e, and row l16 of K^T tile ct
+      // (the A operand of lane l) holds that column ordering already. Two
+      // passes over the blocks: amax, then requantisation (the reference
+      // quantiser, ref:36-37,83-99: s = amax/448, 1 when amax is not > 0;
+      // codes = e4m3fn(clamp(x / s, +-448)) with the unrounded fp32 s).
+      float s32 = 1.f;
+#pragma unroll 1
+      for (int pass = 0; pass < 2; ++pass) {
+        uint32_t am = 0;
+#pragma unroll
+        for (int mm = 0; mm < 2; ++mm) {
+          const int blk = 2 * p + mm;
+          f32x4_t sn[8];
+#pragma unroll
+          for (int ct = 0; ct < 8; ++ct) {
+            const uint4 c = cf[(ct >> 2) * 2 + mm];
+            const uint32_t wd = (ct & 3) == 0 ? c.x : (ct & 3) == 1 ? c.y : (ct & 3) == 2 ? c.z : c.w;
+            float f[4];
+            fp8x4_to_f32(opaque(wd), f);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) sn[ct][e] = lam_all * (f[e] * sc);
+          }
+          const uint4 u = ubuf[mm * 64 + lane];
+          const uint8_t* kt_lane = lds + a.lds_kt + l16 * 16 * ES + 4 * q4 * ES;  // tokens 4 q4 + e
+#pragma unroll
+          for (int ct = 0; ct < 8; ++ct) {
+            const uint8_t* ktrow = kt_lane + ct * 256 * ES;
+            if constexpr (BF16) {
+              const bf16x4_t av = __builtin_bit_cast(bf16x4_t, *(const uint2*)ktrow);
+              sn[ct] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(av, __builtin_bit_cast(bf16x4_t, make_uint2(u.x, u.y)),
+                                                                 sn[ct], 0, 0, 0);
+              sn[ct] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(av, __builtin_bit_cast(bf16x4_t, make_uint2(u.z, u.w)),
+                                                                 sn[ct], 0, 0, 0);
+            } else {
+              const float uf[4] = {__uint_as_float(u.x), __uint_as_float(u.y), __uint_as_float(u.z),
+                                   __uint_as_float(u.w)};
+#pragma unroll
+              for (int e = 0; e < 4; ++e)
+                sn[ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(Act::ld(ktrow, e), uf[e], sn[ct], 0, 0, 0);
+            }
+          }
+          if (pass == 0) {
+#pragma unroll
+            for (int ct = 0; ct < 8; ++ct)
+#pragma unroll
+              for (int e = 0; e < 4; ++e) am = max(am, __float_as_uint(sn[ct][e]) & 0x7FFFFFFFu);
+          } else {
+            uint8_t* rp = ck_rows + (int64_t)(16 * blk + l16) * a.ck_v + 16 * q4;
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+              uint32_t wd[4];
+#pragma unroll
+              for (int w = 0; w < 4; ++w) {
+                const f32x4_t& v = sn[4 * hh + w];
+                wd[w] = f32x4_to_fp8(clamp448(v[0] / s32), clamp448(v[1] / s32), clamp448(v[2] / s32),
+                                     clamp448(v[3] / s32));
+              }
+              *(uint4*)(rp + 64 * hh) = make_uint4(wd[0], wd[1], wd[2], wd[3]);
+            }
+          }
+        }
+        if (pass == 0) {
+          const float amax = __uint_as_float(wave_max_u32(am));
+          s32 = (amax > 0.0f) ? amax / 448.0f : 1.0f;
+        }
+      }
+      if (lane == 0)
+        scale_hv[(int64_t)((v0 + r0) / kVBlock + p) * a.sc_v] = __builtin_bit_cast(uint16_t, (_Float16)s32);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) cf[i] = cn[i];
+    }
+  }
+  append_token();
+}
+
+#if GDNR_ACT == 0
+using Act = ActBF16;
+#define GDNR_SUFFIX(name) name##_bf16
+#elif GDNR_ACT == 1
+using Act = ActF16;
+#define GDNR_SUFFIX(name) name##_f16
+#else
+using Act = ActF32;
+#define GDNR_SUFFIX(name) name##_f32
+#endif
+
+template <int NCH, bool FUSED, bool GATE_F32>
+void launch_step_variant(const ReplayArgs& a, hipStream_t s) {
+  const dim3 grid((unsigned)(a.n_vt * (a.G / a.gw)), (unsigned)a.H, (unsigned)a.B), block((unsigned)(64 * a.sw));
+  auto kernel = step_kernel<Act, NCH, FUSED, GATE_F32>;
+  if (a.lds_bytes > 64 * 1024) {
+    // gfx950 has 160 KiB of LDS per workgroup; dynamic allocations above
+    // 64 KiB must be enabled per kernel (idempotent, cheap)
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, a.lds_bytes);
+    if (e != hipSuccess) return;  // the launch below reports the error
+  }
+  hipLaunchKernelGGL(kernel, grid, block, a.lds_bytes, s, a);
+}
+
+template <int NCH>
+void launch_step_nch(const ReplayArgs& a, bool fused, bool gate_f32, hipStream_t s) {
+  if (!fused) launch_step_variant<NCH, false, false>(a, s);
+  else if (gate_f32) launch_step_variant<NCH, true, true>(a, s);
+  else launch_step_variant<NCH, true, false>(a, s);
+}
+
+}  // namespace
+
+int GDNR_SUFFIX(launch_step)(const ReplayArgs& a, bool fused, bool gate_f32, void* stream) {
+  hipStream_t s = (hipStream_t)stream;
+  if (a.rpw == 128) launch_step_nch<16>(a, fused, gate_f32, s);
+  else if (a.rpw == 64) launch_step_nch<8>(a, fused, gate_f32, s);
+  else launch_step_nch<4>(a, fused, gate_f32, s);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? 0 : (int)e;
+}
+
+}  // namespace gdnr

@@ -33,6 +33,7 @@ DEVICE_FLAGS = [
 ]
 HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra"]
 ACTS = ("bf16", "f16", "f32")  # activation dtypes, one kernel object each (GDNR_ACT = index)
+KERNEL_SOURCES = ("gdnr_kernels", "gdnr_step")
 
 
 def _run(cmd: list[str], verbose: bool) -> None:
@@ -50,10 +51,13 @@ def _run(cmd: list[str], verbose: bool) -> None:
 def build(verbose: bool = False) -> Path:
     BUILD_DIR.mkdir(exist_ok=True)
     inc = [f"-I{INCLUDE}", f"-I{CSRC}"]
-    kern_objs = [BUILD_DIR / f"gdnr_kernels_{act}.o" for act in ACTS]
+    kern_objs, jobs = [], []
+    for src in KERNEL_SOURCES:
+        for i, act in enumerate(ACTS):
+            obj = BUILD_DIR / f"{src}_{act}.o"
+            kern_objs.append(obj)
+            jobs.append([HIPCC, *DEVICE_FLAGS, *inc, f"-DGDNR_ACT={i}", "-c", str(CSRC / f"{src}.hip"), "-o", str(obj)])
     abi_obj = BUILD_DIR / "gdnr_abi.o"
-    jobs = [[HIPCC, *DEVICE_FLAGS, *inc, f"-DGDNR_ACT={i}", "-c", str(CSRC / "gdnr_kernels.hip"), "-o", str(obj)]
-            for i, obj in enumerate(kern_objs)]
     jobs.append(["g++", *HOST_FLAGS, *inc, "-c", str(CSRC / "gdnr_abi.cpp"), "-o", str(abi_obj)])
     with ThreadPoolExecutor(max_workers=len(jobs)) as pool:
         for future in [pool.submit(_run, cmd, verbose) for cmd in jobs]:
@@ -65,13 +69,14 @@ def build(verbose: bool = False) -> Path:
     return LIBRARY
 
 
-def device_assembly(act: str = "bf16", out: Path | None = None, verbose: bool = False) -> Path:
-    """Write the gfx950 assembly of one activation dtype's kernels (for the
-    ISA contract tests)."""
-    out = out or BUILD_DIR / f"gdnr_kernels_{act}.s"
+def device_assembly(act: str = "bf16", src: str = "gdnr_step", out: Path | None = None,
+                    verbose: bool = False) -> Path:
+    """Write the gfx950 assembly of one source file's kernels for one
+    activation dtype (inspection of waits, VGPR counts, instruction mix)."""
+    out = out or BUILD_DIR / f"{src}_{act}.s"
     BUILD_DIR.mkdir(exist_ok=True)
     _run([HIPCC, *DEVICE_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", f"-DGDNR_ACT={ACTS.index(act)}", "--cuda-device-only",
-          "-S", str(CSRC / "gdnr_kernels.hip"), "-o", str(out)], verbose)
+          "-S", str(CSRC / f"{src}.hip"), "-o", str(out)], verbose)
     return out
 
 
