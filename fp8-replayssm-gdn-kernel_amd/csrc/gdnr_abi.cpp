@@ -224,7 +224,7 @@ int fit_lds(gdnr::ReplayArgs* a, int es, bool stage_k, bool stage_v) {
 }
 
 // LDS plan of the step kernel (gdnr_step.hip, L <= kStepRing) for the
-// current gw / block_v: q | new k | k ring | flags | c_t | T0 | slot Gram per head |
+// current gw / block_v: q | new k | k ring | flags | w | T0 | slot Gram per head |
 // v rows | flush: R | factors | K^T tiles | lam_all | U~/W tiles.
 int32_t layout_step(gdnr::ReplayArgs* a, int es) {
   const int64_t K = gdnr::kKeyDim, LP = gdnr::kStepRing;
@@ -238,10 +238,10 @@ int32_t layout_step(gdnr::ReplayArgs* a, int es) {
   region(&a->lds_q, K * es);
   region(&a->lds_knew, K * es);
   region(&a->lds_k, (int64_t)a->L * K * es);
-  region(&a->lds_flag, (int64_t)a->gw * 8);
-  region(&a->lds_c, (int64_t)a->gw * LP * 4);
+  region(&a->lds_flag, (int64_t)a->gw * 20);  // 3 flags + new (gamma, beta) per head
+  region(&a->lds_c, (int64_t)a->gw * a->block_v * 4);  // w = sum_t c_t v_t per row
   region(&a->lds_t, (int64_t)a->gw * K * 4);
-  region(&a->lds_g, (int64_t)a->gw * (LP + 2) * (LP + 3) * 4);  // [slots, q, new k]^2, stride 19
+  region(&a->lds_g, (int64_t)a->gw * (LP + 2) * 20 * 4);  // [slots, q, new k]^2, row stride 20
   region(&a->lds_v, (int64_t)a->gw * LP * a->rpw * es);
   region(&a->lds_r, (int64_t)a->gw * LP * LP * 4);
   region(&a->lds_fac, (int64_t)a->gw * LP * 16);
@@ -270,12 +270,76 @@ int fit_step(gdnr::ReplayArgs* a, int es) {
   return fail(GDNR_ERR_UNSUPPORTED, "no step-kernel tiling fits (V=%d, G=%d)", a->V, a->G);
 }
 
-// The step kernel forms per-lane ring / checkpoint offsets in 32 bits and
-// moves v-ring rows (and the new token's v) in pairs of elements.
+// The step kernel moves v-ring rows (and the new token's v) in pairs of
+// elements and forms every address as a 32-bit byte offset from a tensor's
+// base pointer: it takes tensors whose byte extent (largest reachable offset)
+// is below 2^31.
 bool step_offsets_fit(const gdnr::ReplayArgs& a, int es) {
-  const int64_t lim = (int64_t)1 << 31;
   const bool pairs = a.v_b % 2 == 0 && a.v_t % 2 == 0 && a.v_h % 2 == 0 && (a.mixed == nullptr || a.mx_b % 2 == 0);
-  return pairs && (int64_t)a.L * a.k_t * es < lim && (int64_t)a.L * a.v_t * es < lim && (int64_t)a.V * a.ck_v < lim;
+  if (!pairs) return false;
+  const int64_t lim = (int64_t)1 << 31;
+  const int64_t B = a.B, L = a.L, HV = a.HV, H = a.H, V = a.V, K = gdnr::kKeyDim;
+  auto fits = [lim](int64_t extent_bytes) { return extent_bytes >= 0 && extent_bytes < lim; };
+  bool ok = fits(((B - 1) * a.ck_b + (HV - 1) * a.ck_h + (V - 1) * a.ck_v + K)) &&
+            fits(2 * ((B - 1) * a.sc_b + (HV - 1) * a.sc_h + (V / gdnr::kVBlock - 1) * a.sc_v + 1)) &&
+            fits(es * ((B - 1) * a.k_b + (L - 1) * a.k_t + (H - 1) * a.k_h + K)) &&
+            fits(es * ((B - 1) * a.v_b + (L - 1) * a.v_t + (HV - 1) * a.v_h + V)) &&
+            fits(es * ((B - 1) * a.g_b + (L - 1) * a.g_t + (HV - 1) * a.g_h + 1)) &&
+            fits(es * ((B - 1) * a.be_b + (L - 1) * a.be_t + (HV - 1) * a.be_h + 1)) &&
+            fits(es * ((B - 1) * a.o_b + (HV - 1) * a.o_h + V)) && fits(4 * ((B - 1) * a.vl_s + 1)) &&
+            fits((B - 1) * a.fl_s + 4);
+  if (a.mixed) {
+    ok = ok && fits(es * ((B - 1) * a.mx_b + 2 * H * K + HV * V)) && fits(4 * ((B - 1) * a.pos_s + 1)) &&
+         fits(es * ((B - 1) * a.qo_b + (H - 1) * a.qo_h + K)) && fits(4 * ((B - 1) * a.a_b + (HV - 1) * a.a_h + 1)) &&
+         fits(4 * ((B - 1) * a.bg_b + (HV - 1) * a.bg_h + 1)) && fits(4 * ((HV - 1) * a.al_s + 1)) &&
+         fits(4 * ((HV - 1) * a.db_s + 1));
+  } else {
+    ok = ok && fits(es * ((B - 1) * a.q_b + (H - 1) * a.q_h + K));
+  }
+  return ok;
+}
+
+// StepArgs from a validated, fitted ReplayArgs (element strides -> byte strides).
+gdnr::StepArgs make_step_args(const gdnr::ReplayArgs& r, int es, int gate_es) {
+  gdnr::StepArgs s = {};
+  s.ckpt = r.ckpt;
+  s.scale = (uint8_t*)r.scale;
+  s.q = (const uint8_t*)r.q;
+  s.k = (uint8_t*)r.k;
+  s.v = (uint8_t*)r.v;
+  s.g = (uint8_t*)r.g;
+  s.beta = (uint8_t*)r.beta;
+  s.out = (uint8_t*)r.out;
+  s.valid_len = (const uint8_t*)r.valid_len;
+  s.flush = r.flush;
+  s.pos = (const uint8_t*)r.pos;
+  s.mixed = (const uint8_t*)r.mixed;
+  s.a = (const uint8_t*)r.a;
+  s.bgate = (const uint8_t*)r.bgate;
+  s.a_log = (const uint8_t*)r.a_log;
+  s.dt_bias = (const uint8_t*)r.dt_bias;
+  s.q_out = (uint8_t*)r.q_out;
+  auto u32 = [](int64_t x) { return (uint32_t)x; };
+  s.ck_b = u32(r.ck_b), s.ck_h = u32(r.ck_h), s.ck_v = u32(r.ck_v);
+  s.sc_b = u32(2 * r.sc_b), s.sc_h = u32(2 * r.sc_h), s.sc_v = u32(2 * r.sc_v);
+  s.q_b = u32(es * r.q_b), s.q_h = u32(es * r.q_h);
+  s.k_b = u32(es * r.k_b), s.k_t = u32(es * r.k_t), s.k_h = u32(es * r.k_h);
+  s.v_b = u32(es * r.v_b), s.v_t = u32(es * r.v_t), s.v_h = u32(es * r.v_h);
+  s.g_b = u32(es * r.g_b), s.g_t = u32(es * r.g_t), s.g_h = u32(es * r.g_h);
+  s.be_b = u32(es * r.be_b), s.be_t = u32(es * r.be_t), s.be_h = u32(es * r.be_h);
+  s.vl_s = u32(4 * r.vl_s), s.fl_s = u32(r.fl_s), s.pos_s = u32(4 * r.pos_s);
+  s.o_b = u32(es * r.o_b), s.o_h = u32(es * r.o_h), s.mx_b = u32(es * r.mx_b);
+  s.a_b = u32(gate_es * r.a_b), s.a_h = u32(gate_es * r.a_h), s.bg_b = u32(gate_es * r.bg_b),
+  s.bg_h = u32(gate_es * r.bg_h);
+  s.al_s = u32(4 * r.al_s), s.db_s = u32(4 * r.db_s);
+  s.qo_b = u32(es * r.qo_b), s.qo_h = u32(es * r.qo_h);
+  s.B = r.B, s.H = r.H, s.G = r.G, s.V = r.V, s.L = r.L, s.gw = r.gw, s.block_v = r.block_v, s.n_vt = r.n_vt;
+  s.sw = r.sw, s.rpw = r.rpw;
+  s.out_scale = r.out_scale;
+  s.lds_q = r.lds_q, s.lds_knew = r.lds_knew, s.lds_k = r.lds_k, s.lds_flag = r.lds_flag, s.lds_c = r.lds_c;
+  s.lds_t = r.lds_t, s.lds_g = r.lds_g, s.lds_v = r.lds_v, s.lds_r = r.lds_r, s.lds_fac = r.lds_fac;
+  s.lds_kt = r.lds_kt, s.lds_lam = r.lds_lam, s.lds_u = r.lds_u, s.lds_bytes = r.lds_bytes;
+  return s;
 }
 
 int check_checkpoint(const gdnr_tensor* checkpoint, const gdnr_tensor* scale, const Geometry& g) {
@@ -361,7 +425,8 @@ int launch_replay(const gdnr::ReplayArgs& a, int act, int mode, bool gate_f32, v
   if (act == GDNR_DTYPE_F16) return gdnr::launch_replay_f16(a, mode, gate_f32, stream);
   return gdnr::launch_replay_f32(a, mode, gate_f32, stream);
 }
-int launch_step(const gdnr::ReplayArgs& a, int act, bool fused, bool gate_f32, void* stream) {
+int launch_step(const gdnr::ReplayArgs& r, int act, bool fused, bool gate_f32, void* stream) {
+  const gdnr::StepArgs a = make_step_args(r, elem_size(act), gate_f32 ? 4 : elem_size(act));
   if (act == GDNR_DTYPE_BF16) return gdnr::launch_step_bf16(a, fused, gate_f32, stream);
   if (act == GDNR_DTYPE_F16) return gdnr::launch_step_f16(a, fused, gate_f32, stream);
   return gdnr::launch_step_f32(a, fused, gate_f32, stream);

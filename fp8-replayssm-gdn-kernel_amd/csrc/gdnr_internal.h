@@ -65,6 +65,24 @@ struct ReplayArgs {
 constexpr int32_t kMaxStepLds = 160 * 1024;  // gfx950 LDS per workgroup
 constexpr int kStepRing = 16;                // ring capacity handled by the step kernel
 
+// Argument block of the step kernel (gdnr_step.hip), built on the host from a
+// validated ReplayArgs: byte pointers and 32-bit BYTE strides (the host checks
+// that every tensor's byte extent fits), so that address arithmetic is 32-bit
+// scalar work and the block stays small enough to live in SGPRs.
+struct StepArgs {
+  uint8_t* ckpt; uint8_t* scale;  // scale: fp16 bits
+  const uint8_t* q; uint8_t* k; uint8_t* v; uint8_t* g; uint8_t* beta; uint8_t* out;
+  const uint8_t* valid_len; const uint8_t* flush; const uint8_t* pos;  // flush: nullptr = never
+  const uint8_t* mixed; const uint8_t* a; const uint8_t* bgate; const uint8_t* a_log; const uint8_t* dt_bias;
+  uint8_t* q_out;
+  uint32_t ck_b, ck_h, ck_v, sc_b, sc_h, sc_v, q_b, q_h, k_b, k_t, k_h, v_b, v_t, v_h;
+  uint32_t g_b, g_t, g_h, be_b, be_t, be_h, vl_s, fl_s, pos_s, o_b, o_h, mx_b;
+  uint32_t a_b, a_h, bg_b, bg_h, al_s, db_s, qo_b, qo_h;
+  int32_t B, H, G, V, L, gw, block_v, n_vt, sw, rpw;
+  float out_scale;
+  int32_t lds_q, lds_knew, lds_k, lds_flag, lds_c, lds_t, lds_g, lds_v, lds_r, lds_fac, lds_kt, lds_lam, lds_u, lds_bytes;
+};
+
 struct PrepArgs {
   const void* mixed; int64_t mx_b;
   const void* a; int64_t a_b, a_h;
@@ -97,7 +115,7 @@ enum ReplayMode : int { kModeReplay = 0, kModeApply = 1, kModeFused = 2 };
   int launch_replay_##SUFFIX(const ReplayArgs& a, int mode, bool gate_f32, void* stream); \
   int launch_precompute_##SUFFIX(const ReplayArgs& a, void* stream);                      \
   int launch_prep_##SUFFIX(const PrepArgs& a, bool gate_f32, void* stream);                \
-  int launch_step_##SUFFIX(const ReplayArgs& a, bool fused, bool gate_f32, void* stream);
+  int launch_step_##SUFFIX(const StepArgs& a, bool fused, bool gate_f32, void* stream);
 GDNR_DECLARE_LAUNCHERS(bf16)
 GDNR_DECLARE_LAUNCHERS(f16)
 GDNR_DECLARE_LAUNCHERS(f32)

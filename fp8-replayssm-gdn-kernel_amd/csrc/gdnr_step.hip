@@ -68,12 +68,15 @@ __device__ __forceinline__ uint32_t opaque(uint32_t x) {
   asm volatile("" : "+v"(x));
   return x;
 }
-// 16-bit value at a wave-uniform address, through the scalar cache: the
-// aligned dword holding it (allocations are at least 4-byte granular).
+// Loads at wave-uniform addresses of data the kernel does not write before
+// reading it, through the scalar cache (constant address space): they count
+// in lgkmcnt, so waiting for them never waits for the vector loads.
+typedef __attribute__((address_space(4))) const uint32_t const_u32;
+__device__ __forceinline__ uint32_t ld_u32_uniform(const void* p) { return *(const_u32*)p; }
+// 16-bit value: the aligned dword holding it (allocations are at least 4-byte granular)
 __device__ __forceinline__ uint32_t ld_u16_uniform(const uint16_t* p) {
   const uintptr_t ad = (uintptr_t)p;
-  const uint32_t w = *(const uint32_t*)(ad & ~(uintptr_t)3);
-  return __builtin_amdgcn_readfirstlane((w >> (8u * (uint32_t)(ad & 2))) & 0xFFFFu);
+  return (ld_u32_uniform((const void*)(ad & ~(uintptr_t)3)) >> (8u * (uint32_t)(ad & 2))) & 0xFFFFu;
 }
 // DPP move within a 16-lane row; lanes whose source is outside the row get `fill`.
 template <int CTRL>
@@ -114,91 +117,19 @@ struct XRows {
   }
 };
 
-// One 16x16 tile of X_I X_J^T over K = 128 (rows ri, rj of this lane; rows
-// beyond n are zero). Result element e of lane l is D[4*(l/16) + e][l % 16].
-// bf16/f16: v_mfma_f32_16x16x32, lane l supplying row l % 16 and one 16-byte
-// chunk (8 columns) per instruction; the chunk order is the same for both
-// operands, which is all a Gram product needs.
-template <class Act>
-__device__ __forceinline__ f32x4_t gram_tile(const uint8_t* lds, const XRows& xr, int ri, int rj, int lane) {
-  constexpr int ROWB = K * Act::kBytes;
-  const int q4 = lane >> 4;
-  const bool zi = ri > xr.n, zj = rj > xr.n;
-  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-  if constexpr (std::is_same<Act, ActF32>::value) {
-#pragma unroll
-    for (int kc = 0; kc < K / 4; ++kc) {
-      float av = *(const float*)(lds + xr.off<ROWB>(ri, (kc * 4 + q4) * 4));
-      float bv = *(const float*)(lds + xr.off<ROWB>(rj, (kc * 4 + q4) * 4));
-      av = zi ? 0.f : av;
-      bv = zj ? 0.f : bv;
-      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc, 0, 0, 0);
-    }
-  } else {
-#pragma unroll
-    for (int m = 0; m < K / 32; ++m) {
-      uint4 av = *(const uint4*)(lds + xr.off<ROWB>(ri, (4 * m + q4) * 16));
-      uint4 bv = *(const uint4*)(lds + xr.off<ROWB>(rj, (4 * m + q4) * 16));
-      if (zi) av = make_uint4(0u, 0u, 0u, 0u);
-      if (zj) bv = make_uint4(0u, 0u, 0u, 0u);
-      if constexpr (std::is_same<Act, ActBF16>::value)
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, av), __builtin_bit_cast(bf16x8_t, bv),
-                                                      acc, 0, 0, 0);
-      else
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, av), __builtin_bit_cast(f16x8_t, bv),
-                                                     acc, 0, 0, 0);
-    }
-  }
-  return acc;
-}
-
-// The same tile over the slot rows Y = [ring slots 0..15, q, new k] (18 rows;
-// slots >= L, the new k when not fused and rows beyond 17 are zero), which
-// needs no per-sequence metadata: the chain later picks rows by (n, pos).
-template <class Act, bool FUSED>
-__device__ __forceinline__ f32x4_t gram_tile_slots(const uint8_t* lds, int lds_k, int lds_q, int lds_knew, int L, int ri,
-                                                   int rj, int lane) {
-  constexpr int ROWB = K * Act::kBytes;
-  const int q4 = lane >> 4;
-  auto row_off = [&](int x, int by) { return x < 16 ? lds_k + kr_off<ROWB>(x, by) : (x == 16 ? lds_q : lds_knew) + by; };
-  auto zero_row = [&](int x) { return x < 16 ? x >= L : (x == 17 ? !FUSED : x > 17); };
-  const bool zi = zero_row(ri), zj = zero_row(rj);
-  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-  if constexpr (std::is_same<Act, ActF32>::value) {
-#pragma unroll
-    for (int kc = 0; kc < K / 4; ++kc) {
-      float av = *(const float*)(lds + row_off(ri, (kc * 4 + q4) * 4));
-      float bv = *(const float*)(lds + row_off(rj, (kc * 4 + q4) * 4));
-      av = zi ? 0.f : av;
-      bv = zj ? 0.f : bv;
-      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc, 0, 0, 0);
-    }
-  } else {
-#pragma unroll
-    for (int m = 0; m < K / 32; ++m) {
-      uint4 av = *(const uint4*)(lds + row_off(ri, (4 * m + q4) * 16));
-      uint4 bv = *(const uint4*)(lds + row_off(rj, (4 * m + q4) * 16));
-      if (zi) av = make_uint4(0u, 0u, 0u, 0u);
-      if (zj) bv = make_uint4(0u, 0u, 0u, 0u);
-      if constexpr (std::is_same<Act, ActBF16>::value)
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, av), __builtin_bit_cast(bf16x8_t, bv),
-                                                      acc, 0, 0, 0);
-      else
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, av), __builtin_bit_cast(f16x8_t, bv),
-                                                     acc, 0, 0, 0);
-    }
-  }
-  return acc;
+template <int ROWB>
+__device__ __forceinline__ int xr_off_row(int lds_k, int lds_knew, int lds_q, int x, int n, int pos, int by) {
+  return x < n ? (x == pos ? lds_knew + by : lds_k + kr_off<ROWB>(x, by)) : lds_q + by;
 }
 
 template <bool GATE_F32, class Act>
-__device__ __forceinline__ float ld_gate(const void* p, int64_t i) {
-  if constexpr (GATE_F32) return ((const float*)p)[i];
-  else return Act::ld(p, i);
+__device__ __forceinline__ float ld_gate(const uint8_t* p) {
+  if constexpr (GATE_F32) return *(const float*)p;
+  else return Act::ld(p, 0);
 }
 
 template <class Act, int NCH, bool FUSED, bool GATE_F32>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void step_kernel(const ReplayArgs a) {
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void step_kernel(const StepArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   constexpr int ES = Act::kBytes;
   constexpr int ROWB = K * ES;          // bytes of one k-ring row
@@ -207,6 +138,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
   constexpr int NVB = NCH / 4;          // 32-row vblocks per wave
   constexpr int CPT_K = ROWB / 16;      // 16-byte chunks per key row
   constexpr int CPT_V = RPW * ES / 16;  // 16-byte chunks of one token's slice of this wave's v rows
+  constexpr int NV_DMA = LP * CPT_V / 64; // v-row DMA instructions for all LP slots
   constexpr bool BF16 = std::is_same<Act, ActBF16>::value;
   constexpr bool F16 = std::is_same<Act, ActF16>::value;
 
@@ -229,22 +161,24 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
   const int L = a.L;
 
   // ---- 0. the head leads publish their coefficients through LDS flags -------------
-  // flags[j]: head j's coefficients are in LDS; flags[gw + j]: its ring has landed
+  // flags[j]: head j's coefficients are in LDS; flags[gw + j]: lead j has
+  // issued its ring loads; flags[2 gw + j]: its share of the k ring has
+  // landed; then the new token's (gamma, beta) per head
   int* flags = (int*)(lds + a.lds_flag);
-  if (wave == 0 && lane < 2 * a.gw) flags[lane] = 0;
+  float* newgates = (float*)(flags + 3 * a.gw);
+  if (wave == 0 && lane < 3 * a.gw) flags[lane] = 0;
   GDNR_WAIT_LGKM0();
   __builtin_amdgcn_s_barrier();  // B0, the only workgroup barrier
 
   // ---- 1. metadata (scalar), then the loads of this wave's role ------------------
-  const int n_raw = a.valid_len[(int64_t)b * a.vl_s];
+  const int n_raw = (int)ld_u32_uniform(a.valid_len + b * a.vl_s);
   int pos_raw = -1;
-  if constexpr (FUSED) pos_raw = a.pos[(int64_t)b * a.pos_s];
-  // flush flag: the aligned dword holding the byte (allocations are at least
-  // 4-byte granular, so it stays in bounds)
+  if constexpr (FUSED) pos_raw = (int)ld_u32_uniform(a.pos + b * a.pos_s);
+  // flush flag: the aligned dword holding the byte
   uint32_t flush_word = 0, flush_shift = 0;
   if (a.flush) {
-    const uintptr_t fa = (uintptr_t)(a.flush + (int64_t)b * a.fl_s);
-    flush_word = *(const uint32_t*)(fa & ~(uintptr_t)3);
+    const uintptr_t fa = (uintptr_t)(a.flush + b * a.fl_s);
+    flush_word = ld_u32_uniform((const void*)(fa & ~(uintptr_t)3));
     flush_shift = 8u * (uint32_t)(fa & 3);
   }
   // per-sequence metadata, read once the wave needs it
@@ -261,51 +195,83 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
     do_flush = __builtin_amdgcn_readfirstlane((flush_word >> flush_shift) & 0xFFu) != 0;
   };
 
-  // ---- 2-4. head lead: new token, Gram, coefficient chain, publish ---------------
-  // The lead loads what the chain needs -- the k ring (all L slots; each lead
-  // loads the whole ring: the second copy lands on identical bytes and hits
-  // in L2), q, the gates of its head -- and raises flags[gw + j] when they
-  // have landed, which starts its streamer: the ring requests of the grid
-  // reach memory ahead of the checkpoint stream.
+  // ---- 2-4. lead of head j: ring, new token, Gram, chain, publish ------------------
+  // The lead first loads what the chain needs -- its share of the k ring (the
+  // 16-byte chunks of all L slots split over the gw leads; slots beyond the
+  // fill are read and ignored), q (lead 0; fused: q and k of the new token in
+  // every lead), the gates of its head -- raises flags[gw + j] when they have
+  // landed (which starts its streamer: the ring requests of the grid reach
+  // memory ahead of the checkpoint stream) and waits for the other leads'
+  // shares. The v rows of its head (the filled slots, once the metadata is
+  // in) follow; the lead folds them into w = sum_t c_t v_t and also appends
+  // the new token to the rings (fused).
+  uint8_t* vbuf = lds + a.lds_v + j_head * LP * RPW * ES;
+  float* wv_head = (float*)(lds + a.lds_c) + j_head * RPW;  // w = sum_t c_t v_t, per row
   if (head_lead) {
     const int j = j_head;
-    typename Act::Pair q_bits{}, k_bits{};
+    typename Act::Pair q_bits{}, k_bits{}, vnew_bits{};
     float a_raw = 0.f, b_raw = 0.f, alog_raw = 0.f, dtb_raw = 0.f;
     typename Act::Bits g_bits = 0, b_bits = 0;
     float q0 = 0.f, q1 = 0.f, k0 = 0.f, k1 = 0.f, gate_new = 0.f, beta_new = 0.f;
-    // loads of the chain (the metadata may still be in flight)
-    const uint8_t* kbase = (const uint8_t*)a.k + ((int64_t)b * a.k_b + (int64_t)h * a.k_h) * ES;
-    const uint32_t kt_bytes = (uint32_t)(a.k_t * ES);
-    // destination chunk p of token t holds source chunk p ^ (t & 15)
-    for (int c0 = 0; c0 < L * CPT_K; c0 += 64) {
-      const int c = c0 + lane;
-      const int t = c / CPT_K, ch = c % CPT_K;
-      if (c < L * CPT_K)
-        __builtin_amdgcn_global_load_lds(kbase + (uint32_t)(t * kt_bytes + 16 * (ch ^ (t & 15))),
-                                         (lds_void_t*)(lds + a.lds_k + c0 * 16), 16, 0, 0);
+    {
+      const uint8_t* kbase = a.k + (b * a.k_b + h * a.k_h);
+      const uint32_t kt_bytes = a.k_t;
+      const int nch = L * CPT_K;
+      const int share = ((nch + a.gw - 1) / a.gw + 63) / 64 * 64;  // whole DMA instructions
+      const int c_end = min(nch, (j + 1) * share);
+      // destination chunk p of token t holds source chunk p ^ (t & 15)
+      for (int c0 = j * share; c0 < c_end; c0 += 64) {
+        const int c = c0 + lane;
+        const int t = c / CPT_K, ch = c % CPT_K;
+        if (c < c_end)
+          __builtin_amdgcn_global_load_lds(kbase + (uint32_t)(t * kt_bytes + 16 * (ch ^ (t & 15))),
+                                           (lds_void_t*)(lds + a.lds_k + c0 * 16), 16, 0, 0);
+      }
     }
     if constexpr (!FUSED) {
-      if (lane < CPT_K) {
-        const uint8_t* qrow = (const uint8_t*)a.q + ((int64_t)b * a.q_b + (int64_t)h * a.q_h) * ES;
+      if (j == 0 && lane < CPT_K) {
+        const uint8_t* qrow = a.q + (b * a.q_b + h * a.q_h);
         __builtin_amdgcn_global_load_lds(qrow + 16 * lane, (lds_void_t*)(lds + a.lds_q), 16, 0, 0);
       }
     } else {
-      const uint8_t* row = (const uint8_t*)a.mixed + (int64_t)b * a.mx_b * ES;
+      // (every load below is unconditional -- lanes past the data read a valid
+      // element and drop it -- so that no branch join forces an early wait)
+      const uint8_t* row = a.mixed + b * a.mx_b;
       q_bits = Act::ld_pair_bits(row + (h * K + 2 * lane) * ES);
       k_bits = Act::ld_pair_bits(row + (a.H * K + h * K + 2 * lane) * ES);
-      if (lane == 0) {
-        a_raw = ld_gate<GATE_F32, Act>(a.a, (int64_t)b * a.a_b + (int64_t)hv * a.a_h);
-        b_raw = ld_gate<GATE_F32, Act>(a.bgate, (int64_t)b * a.bg_b + (int64_t)hv * a.bg_h);
-        alog_raw = a.a_log[(int64_t)hv * a.al_s];
-        dtb_raw = a.dt_bias[(int64_t)hv * a.db_s];
+      a_raw = ld_gate<GATE_F32, Act>(a.a + (b * a.a_b + hv * a.a_h));
+      b_raw = ld_gate<GATE_F32, Act>(a.bgate + (b * a.bg_b + hv * a.bg_h));
+      alog_raw = *(const float*)(a.a_log + hv * a.al_s);
+      dtb_raw = *(const float*)(a.dt_bias + hv * a.db_s);
+    }
+    {
+      const int tl = lane < L ? lane : 0;
+      g_bits = Act::ld_bits(a.g + (b * a.g_b + tl * a.g_t + hv * a.g_h), 0);
+      b_bits = Act::ld_bits(a.beta + (b * a.be_b + tl * a.be_t + hv * a.be_h), 0);
+    }
+    // v rows of head j, all L slots (exactly NV_DMA instructions, lanes past L
+    // masked, so that the waits below can count them), then the new v
+    {
+      const uint8_t* vbase = a.v + (b * a.v_b + hv * a.v_h + v0 * ES);
+      const uint32_t vt_bytes = a.v_t;
+#pragma unroll
+      for (int i = 0; i < NV_DMA; ++i) {
+        const int c = 64 * i + lane;
+        const int t = c / CPT_V, ch = c % CPT_V;
+        if (t < L)
+          __builtin_amdgcn_global_load_lds(vbase + (uint32_t)(t * vt_bytes + 16 * ch),
+                                           (lds_void_t*)(vbuf + 64 * i * 16), 16, 0, 0);
       }
     }
-    if (lane < L) {
-      g_bits = Act::ld_bits(a.g, (int64_t)b * a.g_b + (int64_t)lane * a.g_t + (int64_t)hv * a.g_h);
-      b_bits = Act::ld_bits(a.beta, (int64_t)b * a.be_b + (int64_t)lane * a.be_t + (int64_t)hv * a.be_h);
+    if constexpr (FUSED) {
+      const int vl = lane < RPW / 2 ? lane : 0;
+      vnew_bits = Act::ld_pair_bits(a.mixed + (b * a.mx_b + (2 * a.H * K + hv * a.V + v0 + 2 * vl) * ES));
     }
-    GDNR_WAIT_VMCNT(0);  // ring landed; the metadata may still be in flight
+    // the lead's requests are out: the streamer's checkpoint requests queue behind them
     __hip_atomic_store(flags + a.gw + j, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    GDNR_WAIT_VMCNT(NV_DMA + (FUSED ? 1 : 0));  // this lead's share of the ring (not the v rows) landed
+    __hip_atomic_store(flags + 2 * a.gw + j, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+    read_meta();
     if constexpr (FUSED) {
       // full-contract preparation of the new token's q and k (reference
       // kernel:504-533); every lead writes the same values
@@ -319,46 +285,161 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
       Act::st2(lds + a.lds_q + 2 * lane * ES, q0, q1);
       Act::st2(lds + a.lds_knew + 2 * lane * ES, k0, k1);
     }
-    // gates (gamma = e^g, beta) of the ring slots
+    // gates (gamma = e^g, beta) of the tokens
+    const bool on = lane < n;
     float2 gb = make_float2(1.f, 0.f);
-    if (lane < L) gb = make_float2(expf(Act::from_bits(g_bits)), Act::from_bits(b_bits));
+    if (on) gb = make_float2(expf(Act::from_bits(g_bits)), Act::from_bits(b_bits));
     if constexpr (FUSED) {
       // gates of the new token (reference kernel:534-562)
-      float gn = 0.f, bn = 0.f;
-      if (lane == 0) {
-        const float x = a_raw + dtb_raw;
-        const float sp = x <= 20.0f ? logf(1.0f + expf(x)) : x;  // kernel:560, as written there
-        gn = Act::round(-expf(alog_raw) * sp);
-        bn = Act::round(1.0f / (1.0f + expf(-b_raw)));
-      }
-      gate_new = readlane_fv(gn, 0);
-      beta_new = readlane_fv(bn, 0);
+      // (same inputs in every lane)
+      const float x = a_raw + dtb_raw;
+      const float sp = x <= 20.0f ? logf(1.0f + expf(x)) : x;  // kernel:560, as written there
+      gate_new = readlane_fv(Act::round(-expf(alog_raw) * sp), 0);
+      beta_new = readlane_fv(Act::round(1.0f / (1.0f + expf(-b_raw))), 0);
+      if (on && lane == pos) gb = make_float2(expf(gate_new), beta_new);
     }
-    // Gram of the slot rows Y = [slots 0..15, q, new k]: tiles (0,0), (0,1),
-    // (1,1), of which rows / columns 0..17 are kept ([18 x 18], stride 19)
-    float* G = (float*)(lds + a.lds_g) + j * 18 * 19;
-#pragma unroll 1
-    for (int idx = 0; idx < 3; ++idx) {
-      const int ti = idx == 2 ? 1 : 0, tj = idx == 0 ? 0 : 1;
-      const int ri = ti * 16 + l16, rj = tj * 16 + l16;
-      const f32x4_t d = gram_tile_slots<Act, FUSED>(lds, a.lds_k, a.lds_q, a.lds_knew, L, ri, rj, lane);
+    // the other leads' shares of the k ring (bounded waits: every lead raises its flag)
+    for (int jj = 0; jj < a.gw; ++jj)
+      for (int it = 0; it < (1 << 22); ++it) {
+        if (__hip_atomic_load(flags + 2 * a.gw + jj, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) != 0) break;
+        __builtin_amdgcn_s_sleep(1);
+      }
+
+    // Gram of the slot rows Y = [slots 0..15, q, new k]: D00 = slots x slots,
+    // D01 = slots x [q, new k], D11 = [q, new k] x [q, new k], from one read of
+    // each operand row; G [18][20] (row r, column c) with q at 16, new k at 17.
+    float* G = (float*)(lds + a.lds_g) + j * 18 * 20;
+    {
+      const int n_extra = FUSED ? 2 : 1;
+      const bool zs = l16 >= L, ze = l16 >= n_extra;
+      const int erow = l16 == 1 ? a.lds_knew : a.lds_q;
+      f32x4_t d00 = {0.f, 0.f, 0.f, 0.f}, d01 = d00, d11 = d00;
+      if constexpr (std::is_same<Act, ActF32>::value) {
+#pragma unroll 4
+        for (int kc = 0; kc < K / 4; ++kc) {
+          float ka = *(const float*)(lds + a.lds_k + kr_off<ROWB>(l16, (kc * 4 + q4) * 4));
+          float ea = *(const float*)(lds + erow + (kc * 4 + q4) * 4);
+          ka = zs ? 0.f : ka;
+          ea = ze ? 0.f : ea;
+          d00 = __builtin_amdgcn_mfma_f32_16x16x4f32(ka, ka, d00, 0, 0, 0);
+          d01 = __builtin_amdgcn_mfma_f32_16x16x4f32(ka, ea, d01, 0, 0, 0);
+          d11 = __builtin_amdgcn_mfma_f32_16x16x4f32(ea, ea, d11, 0, 0, 0);
+        }
+      } else {
+        uint4 ka[4], ea[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int r = ti * 16 + 4 * q4 + e;
-        if (r < 18 && rj < 18) {
-          G[r * 19 + rj] = d[e];
-          G[rj * 19 + r] = d[e];
+        for (int m = 0; m < 4; ++m) {
+          ka[m] = *(const uint4*)(lds + a.lds_k + kr_off<ROWB>(l16, (4 * m + q4) * 16));
+          ea[m] = *(const uint4*)(lds + erow + (4 * m + q4) * 16);
+        }
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          if (zs) ka[m] = make_uint4(0u, 0u, 0u, 0u);
+          if (ze) ea[m] = make_uint4(0u, 0u, 0u, 0u);
+          if constexpr (std::is_same<Act, ActBF16>::value) {
+            const bf16x8_t ak = __builtin_bit_cast(bf16x8_t, ka[m]), ae = __builtin_bit_cast(bf16x8_t, ea[m]);
+            d00 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak, ak, d00, 0, 0, 0);
+            d01 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak, ae, d01, 0, 0, 0);
+            d11 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ae, ae, d11, 0, 0, 0);
+          } else {
+            const f16x8_t ak = __builtin_bit_cast(f16x8_t, ka[m]), ae = __builtin_bit_cast(f16x8_t, ea[m]);
+            d00 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ak, ak, d00, 0, 0, 0);
+            d01 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ak, ae, d01, 0, 0, 0);
+            d11 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ae, ae, d11, 0, 0, 0);
+          }
+        }
+      }
+      // D[4 q4 + e][l16]: D00 is symmetric, so lane l writes row l16, columns 4 q4 .. + 3
+      *(float4*)(G + l16 * 20 + 4 * q4) = make_float4(d00[0], d00[1], d00[2], d00[3]);
+      if (l16 < 2) {
+        // column 16 + l16 of rows 4 q4 + e, and its mirror (row 16 + l16)
+        *(float4*)(G + (16 + l16) * 20 + 4 * q4) = make_float4(d01[0], d01[1], d01[2], d01[3]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) G[(4 * q4 + e) * 20 + 16 + l16] = d01[e];
+        if (q4 == 0) {
+          G[16 * 20 + 16 + l16] = d11[0];
+          G[17 * 20 + 16 + l16] = d11[1];
         }
       }
     }
-    read_meta();
-    const XRows xr{a.lds_k, a.lds_knew, a.lds_q, n, pos};
-    // token t < n is slot t, except the new token (row 17) at t == pos; q is row 16
-    const bool on = lane < n;
-    if (FUSED && lane == pos) gb = make_float2(expf(gate_new), beta_new);
-    if (!on) gb = make_float2(1.f, 0.f);
-    const int my_row = lane == pos ? 17 : l16;
-    if (do_flush) {
+    // lane t < 16: row of token t (the new k's row at t == pos); columns by token
+    float grow[20];
+    {
+      const float4* gr = (const float4*)(G + (lane == pos ? 17 : l16) * 20);
+#pragma unroll
+      for (int i = 0; i < 5; ++i) {
+        const float4 v4 = gr[i];
+        grow[4 * i] = v4.x;
+        grow[4 * i + 1] = v4.y;
+        grow[4 * i + 2] = v4.z;
+        grow[4 * i + 3] = v4.w;
+      }
+    }
+    float gcol[LP];  // G[token lane][token t], zero for t >= n
+#pragma unroll
+    for (int t = 0; t < LP; ++t) gcol[t] = t < n ? (t == pos ? grow[17] : grow[t]) : 0.f;
+    const float dq = on ? grow[16] : 0.f;
+    // prod_{x >= t} gamma_x (inclusive suffix) and prod_{x > t} gamma_x
+    const float suf_in = row_suffix_prod(gb.x);
+    const float suf_ex = dpp_row<0x101>(suf_in, 1.f);
+    const float lam_all = readlane_fv(suf_in, 0);
+    GDNR_WAIT_VMCNT(0);  // v rows and the new v landed
+    if constexpr (FUSED) {
+      if (pos >= 0 && lane < RPW / 2) {
+        const float2 vn = Act::from_pair(vnew_bits);
+        Act::st2(vbuf + (pos * RPW + 2 * lane) * ES, vn.x, vn.y);
+      }
+    }
+    if (!do_flush) {
+      // s_t, t descending: acc_l = sum_{u > t} G[l][u] s_u (s_t = 0 for t >= n: beta = 0)
+      float acc = 0.f, s_mine = 0.f;
+      const float beta = gb.y;
+#pragma unroll
+      for (int t = LP - 1; t >= 0; --t) {
+        const float sv = readlane_fv(beta * (dq - acc), t);
+        s_mine = lane == t ? sv : s_mine;
+        acc = fmaf(gcol[t], sv, acc);
+      }
+      const float c_mine = on ? s_mine * suf_ex : 0.f;
+      // s and c to LDS (this head's T0 area, overwritten below) and back as
+      // VGPR broadcasts: no SGPRs held across the loop
+      float* sc_lds = (float*)(lds + a.lds_t) + j * K;
+      if (lane < LP) {
+        sc_lds[lane] = s_mine;
+        sc_lds[LP + lane] = c_mine;
+      }
+      float sb[LP], cb[LP];
+#pragma unroll
+      for (int i = 0; i < LP / 4; ++i) {
+        const float4 s4 = ((const float4*)sc_lds)[i], c4 = ((const float4*)(sc_lds + LP))[i];
+        sb[4 * i] = s4.x, sb[4 * i + 1] = s4.y, sb[4 * i + 2] = s4.z, sb[4 * i + 3] = s4.w;
+        cb[4 * i] = c4.x, cb[4 * i + 1] = c4.y, cb[4 * i + 2] = c4.z, cb[4 * i + 3] = c4.w;
+      }
+      // w = sum_t c_t v_t over this head's rows (2 lane, 2 lane + 1), and
+      // T0 = lam_all (q - sum_t s_t k_t), lane owns columns 2 lane, 2 lane + 1
+      // (all 2 x 16 operand pairs are read first, then the FMAs)
+      float2 kk[LP], vv[LP];
+      const int vl = lane < RPW / 2 ? lane : 0;
+#pragma unroll
+      for (int t = 0; t < LP; ++t) {
+        kk[t] = Act::ld2(lds + xr_off_row<ROWB>(a.lds_k, a.lds_knew, a.lds_q, t, n, pos, 2 * lane * ES));
+        vv[t] = Act::ld2(vbuf + (t * RPW + 2 * vl) * ES);
+      }
+      float2 wacc = make_float2(0.f, 0.f);
+      float2 U = Act::ld2(lds + a.lds_q + 2 * lane * ES);
+#pragma unroll
+      for (int t = 0; t < LP; ++t) {
+        const float ct = cb[t], st = sb[t];
+        const float2 v2 = t < n ? vv[t] : make_float2(0.f, 0.f);
+        wacc.x = fmaf(ct, v2.x, wacc.x);
+        wacc.y = fmaf(ct, v2.y, wacc.y);
+        U.x = fmaf(-st, kk[t].x, U.x);
+        U.y = fmaf(-st, kk[t].y, U.y);
+      }
+      if (lane < RPW / 2) *(float2*)(wv_head + 2 * lane) = wacc;
+      *(float2*)(lds + a.lds_t + (j * K + 2 * lane) * 4) = make_float2(lam_all * U.x, lam_all * U.y);
+    } else {
+      const XRows xr{a.lds_k, a.lds_knew, a.lds_q, n, pos};
       // K^T as MFMA A-operand tiles of 16 K-columns x 16 tokens, tile ct at
       // ct * 256 * ES bytes; row r of tile ct is K column
       // 64 (ct / 4) + 16 (r / 4) + 4 (ct % 4) + r % 4, the column order of the
@@ -389,43 +470,6 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
 #pragma unroll
         for (int i = 0; i < ES; ++i) dst[i] = make_uint4(wd[4 * i], wd[4 * i + 1], wd[4 * i + 2], wd[4 * i + 3]);
       }
-    }
-    const float dq = on ? G[my_row * 19 + 16] : 0.f;
-    // prod_{x >= t} gamma_x (inclusive suffix) and prod_{x > t} gamma_x
-    const float suf_in = row_suffix_prod(gb.x);
-    const float suf_ex = dpp_row<0x101>(suf_in, 1.f);
-    const float lam_all = readlane_fv(suf_in, 0);
-    if (!do_flush) {
-      // s_t, t descending: acc_l = sum_{u > t} G[l][u] s_u
-      float gcol[LP];
-#pragma unroll
-      for (int i = 0; i < LP; ++i) gcol[i] = G[my_row * 19 + (i == pos ? 17 : i)];
-      float acc = 0.f, s_mine = 0.f;
-      const float beta = gb.y;
-#pragma unroll
-      for (int t = LP - 1; t >= 0; --t) {
-        if (t < n) {
-          const float sv = readlane_fv(beta * (dq - acc), t);
-          s_mine = lane == t ? sv : s_mine;
-          acc = fmaf(gcol[t], sv, acc);
-        }
-      }
-      if (lane < LP) ((float*)(lds + a.lds_c))[j * LP + lane] = on ? s_mine * suf_ex : 0.f;
-      // T0 = lam_all (q - sum_t s_t k_t), lane owns columns 2 lane, 2 lane + 1
-      float2 kk[LP];
-#pragma unroll
-      for (int t = 0; t < LP; ++t) kk[t] = Act::ld2(lds + xr.off<ROWB>(t, 2 * lane * ES));
-      float2 U = Act::ld2(lds + a.lds_q + 2 * lane * ES);
-#pragma unroll
-      for (int t = 0; t < LP; ++t) {
-        if (t < n) {
-          const float st = readlane_fv(s_mine, t);
-          U.x = fmaf(-st, kk[t].x, U.x);
-          U.y = fmaf(-st, kk[t].y, U.y);
-        }
-      }
-      *(float2*)(lds + a.lds_t + (j * K + 2 * lane) * 4) = make_float2(lam_all * U.x, lam_all * U.y);
-    } else {
       // flush factors of head j:
       //   pre_t  = prod_{x<=t} gamma_x        post_t = beta_t prod_{x>t} gamma_x
       //   M[t][s] = beta_s prod_{s<x<=t} gamma_x (k_s . k_t)   (s < t)
@@ -436,22 +480,37 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
       if (lane < LP)
         ((float4*)(lds + a.lds_fac))[j * LP + lane] = make_float4(on ? pre : 0.f, on ? post : 0.f, dq, 0.f);
       if (lane == 0) ((float*)(lds + a.lds_lam))[j] = lam_all;
-      // M column s = lane and R column c = lane in registers; R by forward
-      // substitution (I + M) R = I down the rows
-      float mc[LP];
+      // M[t][s] = beta_s prod_{s<x<=t} gamma_x G[s][t] (s < t < n), built with
+      // lane = column s, then R = (I + M)^-1 by forward substitution with lane =
+      // column c. Broadcast operands (gamma, rows of M) go through LDS (this
+      // head's U~ area, unused until the rebuild) into VGPRs.
+      float* bc = (float*)(lds + a.lds_u + j * LP * 192);  // [gamma (16) | M (16 x 16)]
+      if (lane < LP) bc[lane] = gb.x;
+      float gam[LP];
+#pragma unroll
+      for (int i = 0; i < LP / 4; ++i) {
+        const float4 g4 = ((const float4*)bc)[i];
+        gam[4 * i] = g4.x, gam[4 * i + 1] = g4.y, gam[4 * i + 2] = g4.z, gam[4 * i + 3] = g4.w;
+      }
+      float* Mm = bc + LP;
       float run = 1.f;
 #pragma unroll
       for (int t = 0; t < LP; ++t) {
-        const float gt = readlane_fv(gb.x, t);
-        if (t > lane) run *= gt;
-        mc[t] = (lane < t && t < n) ? gb.y * run * G[my_row * 19 + (t == pos ? 17 : t)] : 0.f;
+        if (t > lane) run *= gam[t];
+        if (lane < LP) Mm[t * LP + lane] = (lane < t && t < n) ? gb.y * run * gcol[t] : 0.f;
       }
       float r[LP];
 #pragma unroll
       for (int t = 0; t < LP; ++t) {
+        float mrow[LP];
+#pragma unroll
+        for (int i = 0; i < LP / 4; ++i) {
+          const float4 m4 = ((const float4*)(Mm + t * LP))[i];
+          mrow[4 * i] = m4.x, mrow[4 * i + 1] = m4.y, mrow[4 * i + 2] = m4.z, mrow[4 * i + 3] = m4.w;
+        }
         float x = (t == lane) ? 1.f : 0.f;
 #pragma unroll
-        for (int s2 = 0; s2 < t; ++s2) x = fmaf(-readlane_fv(mc[t], s2), r[s2], x);
+        for (int s2 = 0; s2 < t; ++s2) x = fmaf(-mrow[s2], r[s2], x);
         r[t] = x;
       }
       if (lane < LP) {
@@ -460,68 +519,26 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
         for (int t = 0; t < LP; ++t) Rj[t * LP + lane] = (t < n && on) ? r[t] : 0.f;
       }
     }
-    // publish: this head's coefficients (and the shared q / new k / K^T) are in LDS
-    __hip_atomic_store(flags + j, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
-    if constexpr (FUSED) {
-      // ring append of the new token's q (output), k and gates
-      if (j == 0 && vt == 0 && sub == 0) {
-        uint8_t* qo = (uint8_t*)a.q_out + ((int64_t)b * a.qo_b + (int64_t)h * a.qo_h) * ES;
-        Act::st2(qo + 2 * lane * ES, q0, q1);
-        if (pos >= 0) {
-          uint8_t* kr_out = (uint8_t*)a.k + ((int64_t)b * a.k_b + (int64_t)pos * a.k_t + (int64_t)h * a.k_h) * ES;
-          Act::st2(kr_out + 2 * lane * ES, k0, k1);
-        }
-      }
-      if (vt == 0 && pos >= 0 && lane == 0) {
-        Act::st(a.g, (int64_t)b * a.g_b + (int64_t)pos * a.g_t + (int64_t)hv * a.g_h, gate_new);
-        Act::st(a.beta, (int64_t)b * a.be_b + (int64_t)pos * a.be_t + (int64_t)hv * a.be_h, beta_new);
-      }
+    // the new token's gates, for the streamer's ring append
+    if (FUSED && lane == 0) {
+      newgates[2 * j] = gate_new;
+      newgates[2 * j + 1] = beta_new;
     }
+    // publish: this head's coefficients, w (or flush factors), v rows, new
+    // gates and the shared q / new k / K^T are in LDS
+    __hip_atomic_store(flags + j, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
     return;
   }
+
   // ---- streamer of head j_head ---------------------------------------------------
-  // this wave's rows: v rows (all L slots) -> LDS, the new v (fused), the
-  // vblock scales, then (replay) the checkpoint rows: ck[hh * NBLK + i] = row
-  // 16 i + l16, bytes [64 hh + 16 q4, +16); word w of it holds columns
-  // 64 hh + 16 q4 + 4 w + e
-  uint8_t* vbuf = lds + a.lds_v + j_head * LP * RPW * ES;
-  uint16_t* scale_hv = a.scale + (int64_t)b * a.sc_b + (int64_t)hv * a.sc_h;
-  uint8_t* ck_rows = a.ckpt + (int64_t)b * a.ck_b + (int64_t)hv * a.ck_h + (int64_t)(v0 + r0) * a.ck_v;
-  typename Act::Pair vnew_bits{};  // rows 2 lane, 2 lane + 1 of the new v
-  uint32_t sc_bits[NVB];  // scalar
-  uint4 ck[NCH];
-  auto issue_rows = [&]() {
-    const uint8_t* vbase = (const uint8_t*)a.v + ((int64_t)b * a.v_b + (int64_t)hv * a.v_h + v0 + r0) * ES;
-    const uint32_t vt_bytes = (uint32_t)(a.v_t * ES);
-    for (int c0 = 0; c0 < L * CPT_V; c0 += 64) {
-      const int c = c0 + lane;
-      const int t = c / CPT_V, ch = c % CPT_V;
-      if (c < L * CPT_V)
-        __builtin_amdgcn_global_load_lds(vbase + (uint32_t)(t * vt_bytes + 16 * ch), (lds_void_t*)(vbuf + c0 * 16), 16,
-                                         0, 0);
-    }
-    if constexpr (FUSED) {
-      if (lane < RPW / 2)
-        vnew_bits = Act::ld_pair_bits((const uint8_t*)a.mixed +
-                                      ((int64_t)b * a.mx_b + 2 * a.H * K + hv * a.V + v0 + r0 + 2 * lane) * ES);
-    }
-#pragma unroll
-    for (int p = 0; p < NVB; ++p) sc_bits[p] = ld_u16_uniform(scale_hv + (int64_t)((v0 + r0) / kVBlock + p) * a.sc_v);
-  };
-  // checkpoint rows at a uniform base per 16-row block + one 32-bit lane offset
-  const uint32_t ck_lo = (uint32_t)l16 * (uint32_t)a.ck_v + 16 * q4;
-  auto issue_ck = [&]() {
-    GDNR_COMPILER_FENCE();
-#pragma unroll
-    for (int hh = 0; hh < 2; ++hh)
-#pragma unroll
-      for (int i = 0; i < NBLK; ++i) {
-        const uint8_t* base = ck_rows + (int64_t)(16 * i) * a.ck_v + 64 * hh;
-        ck[hh * NBLK + i] = *(const uint4*)(base + ck_lo);
-      }
-    GDNR_COMPILER_FENCE();
-  };
-  // stream once the lead's ring has landed (bounded wait: the lead always raises the flag)
+  // checkpoint rows (replay): ck[hh * NBLK + i] = row 16 i + l16, bytes
+  // [64 hh + 16 q4, +16); word w of it holds columns 64 hh + 16 q4 + 4 w + e,
+  // at a uniform base per 16-row block + one 32-bit lane offset
+  uint8_t* scale_hv = a.scale + (b * a.sc_b + hv * a.sc_h);
+  uint8_t* ck_rows = a.ckpt + (b * a.ck_b + hv * a.ck_h + (v0 + r0) * a.ck_v);
+  const uint32_t ck_lo = (uint32_t)l16 * a.ck_v + 16 * q4;
+  uint8_t* out_rows = a.out + (b * a.o_b + hv * a.o_h + (v0 + r0) * ES);
+  // stream once the lead's ring requests are out (bounded wait: the lead always raises the flag)
   for (int it = 0; it < (1 << 22); ++it) {
     if (__hip_atomic_load(flags + a.gw + j_head, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != 0) break;
     __builtin_amdgcn_s_sleep(1);
@@ -530,46 +547,63 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
   // requests all of its checkpoint rows now, a flush one vblock at a time in
   // section 7 (its registers go to the rebuild instead).
   read_meta();
-  issue_rows();
-  // ================= all waves: own rows =======================================
-  const int64_t out_base = (int64_t)b * a.o_b + (int64_t)hv * a.o_h + v0 + r0;
-  // ring append of the new token's v rows (full contract): issued last, after every load
-  auto append_token = [&]() {
-    if constexpr (FUSED) {
-      if (pos >= 0 && lane < RPW / 2) {
-        const float2 vn = Act::from_pair(vnew_bits);
-        Act::st2((uint8_t*)a.v + ((int64_t)b * a.v_b + (int64_t)pos * a.v_t + (int64_t)hv * a.v_h + v0 + r0 + 2 * lane) * ES,
-                 vn.x, vn.y);
-      }
-    }
-  };
-
-  // the new v into this head's rows, then wait for the lead's coefficients
+  // wait for this head's lead (bounded: the lead always publishes)
   auto await_coefficients = [&]() {
-    if constexpr (FUSED) {
-      if (pos >= 0 && lane < RPW / 2) {
-        const float2 vn = Act::from_pair(vnew_bits);
-        Act::st2(vbuf + (pos * RPW + 2 * lane) * ES, vn.x, vn.y);
-      }
-    }
-    // wait for this head's lead (bounded: the lead always publishes)
     for (int it = 0; it < (1 << 22); ++it) {
       if (__hip_atomic_load(flags + j_head, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) != 0) break;
       __builtin_amdgcn_s_sleep(1);
     }
   };
-  const XRows xr{a.lds_k, a.lds_knew, a.lds_q, n, pos};
+  // Ring append of the new token (full contract), from what the lead left in
+  // LDS: this head's v rows and gates, and (streamer 0 of the key head's
+  // first workgroup) q (output) and k. Issued after every load of the wave.
+  auto append_token = [&]() {
+    if constexpr (FUSED) {
+      if (pos >= 0) {
+        if (lane < RPW / 2) {
+          const uint32_t vw = *(const uint32_t*)(vbuf + (pos * RPW + 2 * lane) * ES);
+          *(uint32_t*)(a.v + (b * a.v_b + pos * a.v_t + hv * a.v_h + (v0 + 2 * lane) * ES)) = vw;
+          if constexpr (ES == 4)
+            *(uint32_t*)(a.v + (b * a.v_b + pos * a.v_t + hv * a.v_h + (v0 + 2 * lane) * ES + 4)) =
+                *(const uint32_t*)(vbuf + (pos * RPW + 2 * lane) * ES + 4);
+        }
+        if (vt == 0 && lane == 0) {
+          Act::st(a.g + (b * a.g_b + pos * a.g_t + hv * a.g_h), 0, newgates[2 * j_head]);
+          Act::st(a.beta + (b * a.be_b + pos * a.be_t + hv * a.be_h), 0, newgates[2 * j_head + 1]);
+        }
+      }
+      if (j_head == 0 && vt == 0 && sub == 0) {
+        const float2 q2 = Act::ld2(lds + a.lds_q + 2 * lane * ES);
+        Act::st2(a.q_out + (b * a.qo_b + h * a.qo_h + 2 * lane * ES), q2.x, q2.y);
+        if (pos >= 0) {
+          const float2 k2 = Act::ld2(lds + a.lds_knew + 2 * lane * ES);
+          Act::st2(a.k + (b * a.k_b + pos * a.k_t + h * a.k_h + 2 * lane * ES), k2.x, k2.y);
+        }
+      }
+    }
+  };
 
   // The replay and flush tails share no code after this point (each returns),
   // so the checkpoint registers of the replay never meet the registers of the
   // rebuild.
   if (!do_flush) {
-    // ---- replay: o = (scale * codes) . T0 + sum_t c_t v_t -------------------
-    issue_ck();
-    GDNR_WAIT_VMCNT(NCH);  // own v rows, new v and scales landed; checkpoint rows still streaming
+    // ---- replay: o = (scale * codes) . T0 + w -----------------------------------
+    uint32_t sc_bits[NVB];  // scalar
+#pragma unroll
+    for (int p = 0; p < NVB; ++p) sc_bits[p] = ld_u16_uniform((const uint16_t*)(scale_hv + ((v0 + r0) / kVBlock + p) * a.sc_v));
+    uint4 ck[NCH];
+    GDNR_COMPILER_FENCE();
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+      for (int i = 0; i < NBLK; ++i) {
+        const uint8_t* base = ck_rows + (16 * i) * a.ck_v + 64 * hh;
+        ck[hh * NBLK + i] = *(const uint4*)(base + ck_lo);
+      }
+    GDNR_COMPILER_FENCE();
     await_coefficients();
     // lane (l16, q4) holds, per block i, row 16 i + l16 at columns
-    // 64 hh + 16 q4 + [0, 16): partial dots, then a 4-lane butterfly over q4
+    // 64 hh + 16 q4 + [0, 16): partial dots, then a 4-lane butterfly over q4;
     // one half (hh) of the columns at a time: 16 values of T0 in registers
     float P[NBLK];
 #pragma unroll
@@ -614,39 +648,29 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
       R2[m] = keep + __shfl_xor(send, 16);
     }
     constexpr int NOUT = NBLK >= 4 ? NBLK / 4 : 1;
-    float tot[NOUT];
-    int rows[NOUT];
-    if constexpr (NBLK >= 4) {
-#pragma unroll
-      for (int m = 0; m < NOUT; ++m) {
-        const float send = hi2 ? R2[2 * m] : R2[2 * m + 1];
-        const float keep = hi2 ? R2[2 * m + 1] : R2[2 * m];
-        tot[m] = keep + __shfl_xor(send, 32);
-        rows[m] = 64 * m + lane;
-      }
-    } else {
-      tot[0] = R2[0] + __shfl_xor(R2[0], 32);
-      rows[0] = 16 * (q4 & 1) + l16;
-    }
-    const float* cj = (const float*)(lds + a.lds_c) + j_head * LP;
 #pragma unroll
     for (int m = 0; m < NOUT; ++m) {
-      const int row = rows[m];  // row within this head's block_v rows
-      float acc = 0.f;
-#pragma unroll
-      for (int t = 0; t < LP; ++t) {
-        if (t < n) acc = fmaf(readlane_fv(cj[t], 0), Act::ld(vbuf, t * RPW + row), acc);
+      float tot;
+      int row;  // row within this head's block_v rows
+      if constexpr (NBLK >= 4) {
+        const float send = hi2 ? R2[2 * m] : R2[2 * m + 1];
+        const float keep = hi2 ? R2[2 * m + 1] : R2[2 * m];
+        tot = keep + __shfl_xor(send, 32);
+        row = 64 * m + lane;
+      } else {
+        tot = R2[0] + __shfl_xor(R2[0], 32);
+        row = 16 * (q4 & 1) + l16;
       }
       const float sc = f16_bits_to_f32((uint16_t)sc_bits[NVB > 1 ? (row >> 5) : 0]);
-      if (NBLK >= 4 || q4 < 2) Act::st(a.out, out_base + row, fmaf(tot[m], sc, acc) * a.out_scale);
+      if (NBLK >= 4 || q4 < 2) Act::st(out_rows, row, fmaf(tot, sc, wv_head[row]) * a.out_scale);
     }
     append_token();
     return;
   }
 
   // ---- 7. flush: MFMA rebuild of this wave's rows, emit, requantise in place
-  GDNR_WAIT_VMCNT(0);
   await_coefficients();
+  const XRows xr{a.lds_k, a.lds_knew, a.lds_q, n, pos};
   // Per vblock p (32 rows = 16-row blocks 2p, 2p + 1) lane l owns row l % 16
   // of a block; the contraction walks the columns in the order of ck, so every
   // checkpoint operand comes straight from those registers and the
@@ -672,13 +696,13 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
       for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
         for (int mm = 0; mm < 2; ++mm)
-          d[hh * 2 + mm] = *(const uint4*)(ck_rows + (int64_t)(32 * p + 16 * mm) * a.ck_v + 64 * hh + ck_lo);
+          d[hh * 2 + mm] = *(const uint4*)(ck_rows + ((32 * p + 16 * mm) * a.ck_v + 64 * hh + ck_lo));
     };
     load_vb(0, cf);
 #pragma unroll 1
     for (int p = 0; p < NVB; ++p) {
       if (p + 1 < NVB) load_vb(p + 1, cn);
-      const float sc = f16_bits_to_f32((uint16_t)ld_u16_uniform(scale_hv + (int64_t)((v0 + r0) / kVBlock + p) * a.sc_v));
+      const float sc = f16_bits_to_f32((uint16_t)ld_u16_uniform((const uint16_t*)(scale_hv + ((v0 + r0) / kVBlock + p) * a.sc_v)));
 #pragma unroll
       for (int mm = 0; mm < 2; ++mm) {
         const int blk = 2 * p + mm;
@@ -775,7 +799,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
         }
         o_part += __shfl_xor(o_part, 16);
         o_part += __shfl_xor(o_part, 32);
-        if (q4 == 0) Act::st(a.out, out_base + rl, o_part * a.out_scale);
+        if (q4 == 0) Act::st(out_rows, rl, o_part * a.out_scale);
       }
       // C: S_n^T tiles sn[ct] of block mm (ct = 4 hh + w): D row 4 q4 + e of
       // tile ct is column 64 hh + 16 q4 + 4 w + e, and row l16 of K^T tile ct
@@ -825,7 +849,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
 #pragma unroll
               for (int e = 0; e < 4; ++e) am = max(am, __float_as_uint(sn[ct][e]) & 0x7FFFFFFFu);
           } else {
-            uint8_t* rp = ck_rows + (int64_t)(16 * blk + l16) * a.ck_v + 16 * q4;
+            uint8_t* rp = ck_rows + ((16 * blk + l16) * a.ck_v + 16 * q4);
 #pragma unroll
             for (int hh = 0; hh < 2; ++hh) {
               uint32_t wd[4];
@@ -845,7 +869,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
         }
       }
       if (lane == 0)
-        scale_hv[(int64_t)((v0 + r0) / kVBlock + p) * a.sc_v] = __builtin_bit_cast(uint16_t, (_Float16)s32);
+        *(uint16_t*)(scale_hv + ((v0 + r0) / kVBlock + p) * a.sc_v) = __builtin_bit_cast(uint16_t, (_Float16)s32);
 #pragma unroll
       for (int i = 0; i < 4; ++i) cf[i] = cn[i];
     }
@@ -865,7 +889,7 @@ using Act = ActF32;
 #endif
 
 template <int NCH, bool FUSED, bool GATE_F32>
-void launch_step_variant(const ReplayArgs& a, hipStream_t s) {
+void launch_step_variant(const StepArgs& a, hipStream_t s) {
   const dim3 grid((unsigned)(a.n_vt * (a.G / a.gw)), (unsigned)a.H, (unsigned)a.B), block((unsigned)(64 * a.sw));
   auto kernel = step_kernel<Act, NCH, FUSED, GATE_F32>;
   if (a.lds_bytes > 64 * 1024) {
@@ -879,7 +903,7 @@ void launch_step_variant(const ReplayArgs& a, hipStream_t s) {
 }
 
 template <int NCH>
-void launch_step_nch(const ReplayArgs& a, bool fused, bool gate_f32, hipStream_t s) {
+void launch_step_nch(const StepArgs& a, bool fused, bool gate_f32, hipStream_t s) {
   if (!fused) launch_step_variant<NCH, false, false>(a, s);
   else if (gate_f32) launch_step_variant<NCH, true, true>(a, s);
   else launch_step_variant<NCH, true, false>(a, s);
@@ -887,7 +911,7 @@ void launch_step_nch(const ReplayArgs& a, bool fused, bool gate_f32, hipStream_t
 
 }  // namespace
 
-int GDNR_SUFFIX(launch_step)(const ReplayArgs& a, bool fused, bool gate_f32, void* stream) {
+int GDNR_SUFFIX(launch_step)(const StepArgs& a, bool fused, bool gate_f32, void* stream) {
   hipStream_t s = (hipStream_t)stream;
   if (a.rpw == 128) launch_step_nch<16>(a, fused, gate_f32, s);
   else if (a.rpw == 64) launch_step_nch<8>(a, fused, gate_f32, s);
