@@ -289,8 +289,29 @@ def main() -> int:
         result["cpu_baseline"]["gpu_speedup"] = result["cpu_baseline"]["value"] / us_step
     else:
         result["cpu_baseline"] = None
+    if args.profile:
+        calibration_copies(device)
     print(json.dumps(result), flush=True)
     return 0
+
+
+CALIB_BYTES = 64 << 20
+CALIB_COPIES = 4
+
+
+def calibration_copies(device) -> None:
+    """The last GPU work of a --profile run: CALIB_COPIES plain copies of
+    CALIB_BYTES bytes each (every byte read once and written once), which
+    calibrate rocprofv3's FETCH_SIZE / WRITE_SIZE counters to bytes."""
+    import torch
+
+    src = torch.randint(0, 256, (CALIB_BYTES,), dtype=torch.uint8, device=device)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(CALIB_COPIES):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"[bench] {CALIB_COPIES} calibration copies of {CALIB_BYTES} bytes done")
 
 
 if __name__ == "__main__":

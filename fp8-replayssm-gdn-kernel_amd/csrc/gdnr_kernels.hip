@@ -12,8 +12,10 @@
 //      adjoint chain runs while the checkpoint is still in flight;
 //   5. the checkpoint matvec o = (codes . T) * scale on the VALU (no MFMA:
 //      one FMA per byte), rows reduced across 8 lanes with DPP.
-// The order of steps 2-3 is pinned with compiler fences; tests/ checks the
-// emitted ISA keeps exactly NCH vector loads between the last DMA and the wait.
+// The order of steps 2-3 is pinned with compiler fences.
+// These kernels serve rings longer than 16 tokens, the split path, the
+// standalone prep and the quantiser; rings of up to 16 tokens go through the
+// step kernel (gdnr_step.hip).
 //
 // This file is compiled once per activation dtype: GDNR_ACT=0 (bf16, also
 // holds the dtype-free quantiser kernels), 1 (f16), 2 (f32).

@@ -7,18 +7,18 @@
 // Workgroup = gw value heads sharing key head h, block_v V-rows of each, and
 // two waves per head:
 //   lead j (wave j): loads the k ring (all L slots; slots beyond the fill are
-//     read and ignored), q and the gates, prepares the new token (fused),
-//     forms the Gram matrix and the coefficient chain of head j, and
-//     publishes the coefficients through an LDS flag. It loads no checkpoint
-//     row: a wave whose loads back up in the memory pipeline cannot issue
-//     anything else, and the checkpoint stream would stall the chain.
-//   streamer j (wave gw + j): owns the block_v rows of head j -- v rows,
-//     vblock scales and NCH = block_v / 8 checkpoint loads of 16 bytes a lane
-//     in the MFMA operand layout (lane (l16, q4) of 16-row block i holds row
-//     l16, bytes [16 q4, +16) and [64 + 16 q4, +16)), which serves both the
-//     replay matvec and the flush rebuild. It starts streaming once its
-//     lead's ring has landed (so the ring requests of the grid reach memory
-//     first), waits for the coefficients, then emits its rows.
+//     read and ignored), q and the gates, then the v rows of head j; prepares
+//     the new token (fused), forms the Gram matrix and the coefficient chain
+//     of head j, folds the v rows into w = sum_t c_t v_t, and publishes
+//     through an LDS flag. It loads no checkpoint row: a wave whose loads
+//     back up in the memory pipeline cannot issue anything else, and the
+//     checkpoint stream would stall the chain.
+//   streamer j (wave gw + j): owns the block_v rows of head j -- vblock
+//     scales and NCH = block_v / 8 checkpoint loads of 16 bytes a lane in the
+//     MFMA operand layout (lane (l16, q4) of 16-row block i holds row l16,
+//     bytes [16 q4, +16) and [64 + 16 q4, +16)), which serves both the replay
+//     matvec and the flush rebuild. It requests them at once, waits for the
+//     coefficients, then emits its rows and appends the new token.
 //
 // Replay, the adjoint of the reference's reverse chain
 // (prototype/gdn_replayssm_fp8_kernel.py:121-173), in Gram form:
@@ -57,6 +57,7 @@ typedef short bf16x4_t __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));  // 16-byte chunk as a native vector (no memcpy)
 
 __device__ __forceinline__ float readlane_fv(float x, int lane) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), lane));
@@ -122,10 +123,23 @@ __device__ __forceinline__ int xr_off_row(int lds_k, int lds_knew, int lds_q, in
   return x < n ? (x == pos ? lds_knew + by : lds_k + kr_off<ROWB>(x, by)) : lds_q + by;
 }
 
+// Acquire-load of an LDS flag, made wave-uniform: every lane reads the same
+// word, and a uniform loop exit keeps the polling loops out of the CFG
+// structurizer (which would otherwise merge the replay and flush tails).
+__device__ __forceinline__ bool flag_set(int* f) {
+  return __builtin_amdgcn_readfirstlane(__hip_atomic_load(f, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP)) != 0;
+}
+
+// raw bits of a gating input (f32, or the activation dtype) and their value
 template <bool GATE_F32, class Act>
-__device__ __forceinline__ float ld_gate(const uint8_t* p) {
-  if constexpr (GATE_F32) return *(const float*)p;
-  else return Act::ld(p, 0);
+__device__ __forceinline__ uint32_t ld_gate_bits(const uint8_t* p) {
+  if constexpr (GATE_F32) return *(const uint32_t*)p;
+  else return (uint32_t)Act::ld_bits(p, 0);
+}
+template <bool GATE_F32, class Act>
+__device__ __forceinline__ float gate_value(uint32_t bits) {
+  if constexpr (GATE_F32) return __uint_as_float(bits);
+  else return Act::from_bits(bits);
 }
 
 template <class Act, int NCH, bool FUSED, bool GATE_F32>
@@ -138,7 +152,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
   constexpr int NVB = NCH / 4;          // 32-row vblocks per wave
   constexpr int CPT_K = ROWB / 16;      // 16-byte chunks per key row
   constexpr int CPT_V = RPW * ES / 16;  // 16-byte chunks of one token's slice of this wave's v rows
-  constexpr int NV_DMA = LP * CPT_V / 64; // v-row DMA instructions for all LP slots
+  constexpr int NV = LP * CPT_V / 64;   // 16-byte v-row chunks per lead lane, all LP slots
+  constexpr int EPC = 16 / ES;          // elements per chunk
   constexpr bool BF16 = std::is_same<Act, ActBF16>::value;
   constexpr bool F16 = std::is_same<Act, ActF16>::value;
 
@@ -161,16 +176,15 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
   const int L = a.L;
 
   // ---- 0. the head leads publish their coefficients through LDS flags -------------
-  // flags[j]: head j's coefficients are in LDS; flags[gw + j]: lead j has
-  // issued its ring loads; flags[2 gw + j]: its share of the k ring has
-  // landed; then the new token's (gamma, beta) per head
+  // flags[j]: head j's coefficients are in LDS; flags[gw + j]: lead j's
+  // share of the k ring has landed; then the new token's (gamma, beta) per head
   int* flags = (int*)(lds + a.lds_flag);
-  float* newgates = (float*)(flags + 3 * a.gw);
-  if (wave == 0 && lane < 3 * a.gw) flags[lane] = 0;
+  float* newgates = (float*)(flags + 2 * a.gw);
+  if (wave == 0 && lane < 2 * a.gw) flags[lane] = 0;
   GDNR_WAIT_LGKM0();
   __builtin_amdgcn_s_barrier();  // B0, the only workgroup barrier
 
-  // ---- 1. metadata (scalar), then the loads of this wave's role ------------------
+  // ---- 1. metadata (scalar), requested by every wave at once ----------------------
   const int n_raw = (int)ld_u32_uniform(a.valid_len + b * a.vl_s);
   int pos_raw = -1;
   if constexpr (FUSED) pos_raw = (int)ld_u32_uniform(a.pos + b * a.pos_s);
@@ -196,23 +210,25 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
   };
 
   // ---- 2-4. lead of head j: ring, new token, Gram, chain, publish ------------------
-  // The lead first loads what the chain needs -- its share of the k ring (the
-  // 16-byte chunks of all L slots split over the gw leads; slots beyond the
-  // fill are read and ignored), q (lead 0; fused: q and k of the new token in
-  // every lead), the gates of its head -- raises flags[gw + j] when they have
-  // landed (which starts its streamer: the ring requests of the grid reach
-  // memory ahead of the checkpoint stream) and waits for the other leads'
+  // The lead first requests what the chain needs -- its share of the k ring
+  // (the 16-byte chunks of all L slots split over the gw leads by
+  // direct-to-LDS DMA; slots beyond the fill are read and ignored), q (lead
+  // 0; fused: q and k of the new token in every lead), the gates of its head
+  // -- before the workgroup barrier B0, after which the streamers request the
+  // checkpoint: the ring requests of the grid reach memory first. It raises
+  // flags[gw + j] when they have landed and waits for the other leads'
   // shares. The v rows of its head (the filled slots, once the metadata is
-  // in) follow; the lead folds them into w = sum_t c_t v_t and also appends
-  // the new token to the rings (fused).
+  // in) follow into VGPRs: no LDS DMA may be pending while the lead touches
+  // LDS, or every LDS access would wait for it. The lead folds them into
+  // w = sum_t c_t v_t (replay) or stages them in LDS (flush).
   uint8_t* vbuf = lds + a.lds_v + j_head * LP * RPW * ES;
-  float* wv_head = (float*)(lds + a.lds_c) + j_head * RPW;  // w = sum_t c_t v_t, per row
-  if (head_lead) {
+  float* c_head = (float*)(lds + a.lds_c) + j_head * RPW;  // c_t of head j (replay)
+  if (__builtin_amdgcn_readfirstlane((int)head_lead) != 0) {
     const int j = j_head;
-    typename Act::Pair q_bits{}, k_bits{}, vnew_bits{};
-    float a_raw = 0.f, b_raw = 0.f, alog_raw = 0.f, dtb_raw = 0.f;
+    typename Act::Pair q_bits{}, k_bits{};
+    uint32_t a_raw = 0, b_raw = 0;
+    float alog_raw = 0.f, dtb_raw = 0.f;
     typename Act::Bits g_bits = 0, b_bits = 0;
-    float q0 = 0.f, q1 = 0.f, k0 = 0.f, k1 = 0.f, gate_new = 0.f, beta_new = 0.f;
     {
       const uint8_t* kbase = a.k + (b * a.k_b + h * a.k_h);
       const uint32_t kt_bytes = a.k_t;
@@ -239,8 +255,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
       const uint8_t* row = a.mixed + b * a.mx_b;
       q_bits = Act::ld_pair_bits(row + (h * K + 2 * lane) * ES);
       k_bits = Act::ld_pair_bits(row + (a.H * K + h * K + 2 * lane) * ES);
-      a_raw = ld_gate<GATE_F32, Act>(a.a + (b * a.a_b + hv * a.a_h));
-      b_raw = ld_gate<GATE_F32, Act>(a.bgate + (b * a.bg_b + hv * a.bg_h));
+      a_raw = ld_gate_bits<GATE_F32, Act>(a.a + (b * a.a_b + hv * a.a_h));
+      b_raw = ld_gate_bits<GATE_F32, Act>(a.bgate + (b * a.bg_b + hv * a.bg_h));
       alog_raw = *(const float*)(a.a_log + hv * a.al_s);
       dtb_raw = *(const float*)(a.dt_bias + hv * a.db_s);
     }
@@ -249,28 +265,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
       g_bits = Act::ld_bits(a.g + (b * a.g_b + tl * a.g_t + hv * a.g_h), 0);
       b_bits = Act::ld_bits(a.beta + (b * a.be_b + tl * a.be_t + hv * a.be_h), 0);
     }
-    // v rows of head j, all L slots (exactly NV_DMA instructions, lanes past L
-    // masked, so that the waits below can count them), then the new v
-    {
-      const uint8_t* vbase = a.v + (b * a.v_b + hv * a.v_h + v0 * ES);
-      const uint32_t vt_bytes = a.v_t;
-#pragma unroll
-      for (int i = 0; i < NV_DMA; ++i) {
-        const int c = 64 * i + lane;
-        const int t = c / CPT_V, ch = c % CPT_V;
-        if (t < L)
-          __builtin_amdgcn_global_load_lds(vbase + (uint32_t)(t * vt_bytes + 16 * ch),
-                                           (lds_void_t*)(vbuf + 64 * i * 16), 16, 0, 0);
-      }
-    }
-    if constexpr (FUSED) {
-      const int vl = lane < RPW / 2 ? lane : 0;
-      vnew_bits = Act::ld_pair_bits(a.mixed + (b * a.mx_b + (2 * a.H * K + hv * a.V + v0 + 2 * vl) * ES));
-    }
-    // the lead's requests are out: the streamer's checkpoint requests queue behind them
-    __hip_atomic_store(flags + a.gw + j, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    GDNR_WAIT_VMCNT(NV_DMA + (FUSED ? 1 : 0));  // this lead's share of the ring (not the v rows) landed
-    __hip_atomic_store(flags + 2 * a.gw + j, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+    float q0 = 0.f, q1 = 0.f, k0 = 0.f, k1 = 0.f, gate_new = 0.f, beta_new = 0.f;
+    GDNR_WAIT_VMCNT(0);  // this lead's share of the k ring and its small operands landed
+    // (this flag also starts the streamers: the checkpoint stream begins once
+    // the chain's operands are in, and the lead issues no load after it)
+    __hip_atomic_store(flags + a.gw + j, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
     read_meta();
     if constexpr (FUSED) {
       // full-contract preparation of the new token's q and k (reference
@@ -292,16 +291,16 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
     if constexpr (FUSED) {
       // gates of the new token (reference kernel:534-562)
       // (same inputs in every lane)
-      const float x = a_raw + dtb_raw;
+      const float x = gate_value<GATE_F32, Act>(a_raw) + dtb_raw;
       const float sp = x <= 20.0f ? logf(1.0f + expf(x)) : x;  // kernel:560, as written there
       gate_new = readlane_fv(Act::round(-expf(alog_raw) * sp), 0);
-      beta_new = readlane_fv(Act::round(1.0f / (1.0f + expf(-b_raw))), 0);
+      beta_new = readlane_fv(Act::round(1.0f / (1.0f + expf(-gate_value<GATE_F32, Act>(b_raw)))), 0);
       if (on && lane == pos) gb = make_float2(expf(gate_new), beta_new);
     }
     // the other leads' shares of the k ring (bounded waits: every lead raises its flag)
     for (int jj = 0; jj < a.gw; ++jj)
       for (int it = 0; it < (1 << 22); ++it) {
-        if (__hip_atomic_load(flags + 2 * a.gw + jj, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) != 0) break;
+        if (flag_set(flags + a.gw + jj)) break;
         __builtin_amdgcn_s_sleep(1);
       }
 
@@ -383,14 +382,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
     const float suf_in = row_suffix_prod(gb.x);
     const float suf_ex = dpp_row<0x101>(suf_in, 1.f);
     const float lam_all = readlane_fv(suf_in, 0);
-    GDNR_WAIT_VMCNT(0);  // v rows and the new v landed
-    if constexpr (FUSED) {
-      if (pos >= 0 && lane < RPW / 2) {
-        const float2 vn = Act::from_pair(vnew_bits);
-        Act::st2(vbuf + (pos * RPW + 2 * lane) * ES, vn.x, vn.y);
-      }
-    }
-    if (!do_flush) {
+    // (the branch conditions are re-made wave-uniform: the divergence
+    // analysis loses track of values set inside read_meta, and a branch it
+    // takes for divergent is structurised into one path through both tails)
+    if (__builtin_amdgcn_readfirstlane((int)do_flush) == 0) {
       // s_t, t descending: acc_l = sum_{u > t} G[l][u] s_u (s_t = 0 for t >= n: beta = 0)
       float acc = 0.f, s_mine = 0.f;
       const float beta = gb.y;
@@ -415,28 +410,21 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
         sb[4 * i] = s4.x, sb[4 * i + 1] = s4.y, sb[4 * i + 2] = s4.z, sb[4 * i + 3] = s4.w;
         cb[4 * i] = c4.x, cb[4 * i + 1] = c4.y, cb[4 * i + 2] = c4.z, cb[4 * i + 3] = c4.w;
       }
-      // w = sum_t c_t v_t over this head's rows (2 lane, 2 lane + 1), and
+      // c for the streamer's w = sum_t c_t v_t (this head's c area)
+      if (lane < LP) c_head[lane] = c_mine;
       // T0 = lam_all (q - sum_t s_t k_t), lane owns columns 2 lane, 2 lane + 1
-      // (all 2 x 16 operand pairs are read first, then the FMAs)
-      float2 kk[LP], vv[LP];
-      const int vl = lane < RPW / 2 ? lane : 0;
+      // (all 16 operand pairs are read first, then the FMAs)
+      float2 kk[LP];
 #pragma unroll
-      for (int t = 0; t < LP; ++t) {
+      for (int t = 0; t < LP; ++t)
         kk[t] = Act::ld2(lds + xr_off_row<ROWB>(a.lds_k, a.lds_knew, a.lds_q, t, n, pos, 2 * lane * ES));
-        vv[t] = Act::ld2(vbuf + (t * RPW + 2 * vl) * ES);
-      }
-      float2 wacc = make_float2(0.f, 0.f);
       float2 U = Act::ld2(lds + a.lds_q + 2 * lane * ES);
 #pragma unroll
       for (int t = 0; t < LP; ++t) {
-        const float ct = cb[t], st = sb[t];
-        const float2 v2 = t < n ? vv[t] : make_float2(0.f, 0.f);
-        wacc.x = fmaf(ct, v2.x, wacc.x);
-        wacc.y = fmaf(ct, v2.y, wacc.y);
+        const float st = sb[t];
         U.x = fmaf(-st, kk[t].x, U.x);
         U.y = fmaf(-st, kk[t].y, U.y);
       }
-      if (lane < RPW / 2) *(float2*)(wv_head + 2 * lane) = wacc;
       *(float2*)(lds + a.lds_t + (j * K + 2 * lane) * 4) = make_float2(lam_all * U.x, lam_all * U.y);
     } else {
       const XRows xr{a.lds_k, a.lds_knew, a.lds_q, n, pos};
@@ -538,34 +526,77 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
   uint8_t* ck_rows = a.ckpt + (b * a.ck_b + hv * a.ck_h + (v0 + r0) * a.ck_v);
   const uint32_t ck_lo = (uint32_t)l16 * a.ck_v + 16 * q4;
   uint8_t* out_rows = a.out + (b * a.o_b + hv * a.o_h + (v0 + r0) * ES);
-  // stream once the lead's ring requests are out (bounded wait: the lead always raises the flag)
-  for (int it = 0; it < (1 << 22); ++it) {
-    if (__hip_atomic_load(flags + a.gw + j_head, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != 0) break;
-    __builtin_amdgcn_s_sleep(1);
-  }
-  // The metadata (requested at kernel start) decides the load plan: a replay
-  // requests all of its checkpoint rows now, a flush one vblock at a time in
-  // section 7 (its registers go to the rebuild instead).
+  // Stream once the k ring has landed (bounded waits: every lead raises its
+  // flag): the ring requests of the grid reach memory ahead of the checkpoint
+  // stream. A replay consumes the checkpoint rows from registers; a flush
+  // drops them and re-reads one vblock at a time in section 7 (its registers
+  // go to the rebuild instead).
+  for (int jj = 0; jj < a.gw; ++jj)
+    for (int it = 0; it < (1 << 22); ++it) {
+      if (flag_set(flags + a.gw + jj)) break;
+      __builtin_amdgcn_s_sleep(1);
+    }
   read_meta();
+  // v rows of head j first (a replay folds them into w before its matvec):
+  // chunk c = 64 i + lane holds rows
+  // EPC (c % CPT_V) + [0, EPC) of token c / CPT_V. Tokens at or past the fill
+  // re-read slot 0 (a cache hit; dropped below); the new token's slot reads
+  // the new v from mixed_qkv. Every lane loads: the instruction count is static.
+  u32x4_t vch[NV];
+  {
+    const uint8_t* vring = a.v + (b * a.v_b + hv * a.v_h + v0 * ES);
+    const uint32_t vt_bytes = a.v_t;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int c = 64 * i + lane;
+      const int t = c / CPT_V, rc = c % CPT_V;
+      const uint8_t* src = vring + ((uint32_t)(t < n ? t : 0) * vt_bytes + 16u * (uint32_t)rc);
+      if constexpr (FUSED)
+        if (t == pos) src = a.mixed + (b * a.mx_b + (2 * a.H * K + hv * a.V + v0) * ES + 16 * rc);
+      vch[i] = *(const u32x4_t*)src;
+    }
+  }
+  uint32_t sc_bits[NVB];  // scalar
+#pragma unroll
+  for (int p = 0; p < NVB; ++p) sc_bits[p] = ld_u16_uniform((const uint16_t*)(scale_hv + ((v0 + r0) / kVBlock + p) * a.sc_v));
+  uint4 ck[NCH];
+  GDNR_COMPILER_FENCE();
+  {
+    // one uniform base, a 32-bit lane offset per 16-row block
+    const uint32_t rstep = 16u * (uint32_t)a.ck_v;
+#pragma unroll
+    for (int i = 0; i < NBLK; ++i) {
+      const uint32_t off = ck_lo + (uint32_t)i * rstep;
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) ck[hh * NBLK + i] = *(const uint4*)(ck_rows + (off + 64u * hh));
+    }
+  }
+  GDNR_COMPILER_FENCE();
+  // the v rows land ahead of the checkpoint rows: copy them to LDS in
+  // token-major order (chunk c at byte 16 c) and free their registers
+  GDNR_WAIT_VMCNT(NCH);
+#pragma unroll
+  for (int i = 0; i < NV; ++i) *(u32x4_t*)(vbuf + 16 * (64 * i + lane)) = vch[i];
   // wait for this head's lead (bounded: the lead always publishes)
   auto await_coefficients = [&]() {
     for (int it = 0; it < (1 << 22); ++it) {
-      if (__hip_atomic_load(flags + j_head, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) != 0) break;
+      if (flag_set(flags + j_head)) break;
       __builtin_amdgcn_s_sleep(1);
     }
   };
-  // Ring append of the new token (full contract), from what the lead left in
-  // LDS: this head's v rows and gates, and (streamer 0 of the key head's
-  // first workgroup) q (output) and k. Issued after every load of the wave.
+  // Ring append of the new token (full contract): its v rows from this
+  // wave's LDS copy, its gates, and (streamer 0 of the key head's first
+  // workgroup) q (output) and k from what the lead left in LDS. Issued after
+  // every load of the wave.
   auto append_token = [&]() {
     if constexpr (FUSED) {
       if (pos >= 0) {
-        if (lane < RPW / 2) {
-          const uint32_t vw = *(const uint32_t*)(vbuf + (pos * RPW + 2 * lane) * ES);
-          *(uint32_t*)(a.v + (b * a.v_b + pos * a.v_t + hv * a.v_h + (v0 + 2 * lane) * ES)) = vw;
-          if constexpr (ES == 4)
-            *(uint32_t*)(a.v + (b * a.v_b + pos * a.v_t + hv * a.v_h + (v0 + 2 * lane) * ES + 4)) =
-                *(const uint32_t*)(vbuf + (pos * RPW + 2 * lane) * ES + 4);
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+          const int c = 64 * i + lane;
+          if (c / CPT_V == pos)
+            *(u32x4_t*)(a.v + (b * a.v_b + pos * a.v_t + hv * a.v_h + v0 * ES + 16 * (c % CPT_V))) =
+                *(const u32x4_t*)(vbuf + 16 * c);
         }
         if (vt == 0 && lane == 0) {
           Act::st(a.g + (b * a.g_b + pos * a.g_t + hv * a.g_h), 0, newgates[2 * j_head]);
@@ -586,22 +617,39 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
   // The replay and flush tails share no code after this point (each returns),
   // so the checkpoint registers of the replay never meet the registers of the
   // rebuild.
-  if (!do_flush) {
+  if (__builtin_amdgcn_readfirstlane((int)do_flush) == 0) {
     // ---- replay: o = (scale * codes) . T0 + w -----------------------------------
-    uint32_t sc_bits[NVB];  // scalar
-#pragma unroll
-    for (int p = 0; p < NVB; ++p) sc_bits[p] = ld_u16_uniform((const uint16_t*)(scale_hv + ((v0 + r0) / kVBlock + p) * a.sc_v));
-    uint4 ck[NCH];
-    GDNR_COMPILER_FENCE();
-#pragma unroll
-    for (int hh = 0; hh < 2; ++hh)
-#pragma unroll
-      for (int i = 0; i < NBLK; ++i) {
-        const uint8_t* base = ck_rows + (16 * i) * a.ck_v + 64 * hh;
-        ck[hh * NBLK + i] = *(const uint4*)(base + ck_lo);
-      }
-    GDNR_COMPILER_FENCE();
     await_coefficients();
+    // w = sum_t c_t v_t: per-lane partials over the lane's chunks (rows
+    // EPC rc + [0, EPC)), exchanged through LDS (this head's U~ area, unused
+    // by a replay) and summed per output row below
+    const float* part = (const float*)(lds + a.lds_u + j_head * LP * 192);  // [lane][EPC]
+    {
+      float wp[EPC];
+#pragma unroll
+      for (int e = 0; e < EPC; ++e) wp[e] = 0.f;
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        const int t = (64 * i + lane) / CPT_V;
+        const bool live = t < n;
+        const float ct = live ? c_head[live ? t : 0] : 0.f;
+        const u32x4_t vc = *(const u32x4_t*)(vbuf + 16 * (64 * i + lane));
+        const uint32_t wd[4] = {vc[0], vc[1], vc[2], vc[3]};
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          if constexpr (ES == 2) {
+            const float2 f = Act::from_pair(wd[w]);
+            wp[2 * w] = fmaf(ct, live ? f.x : 0.f, wp[2 * w]);
+            wp[2 * w + 1] = fmaf(ct, live ? f.y : 0.f, wp[2 * w + 1]);
+          } else {
+            wp[w] = fmaf(ct, live ? __uint_as_float(wd[w]) : 0.f, wp[w]);
+          }
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < EPC; e += 4)
+        *(float4*)(part + lane * EPC + e) = make_float4(wp[e], wp[e + 1], wp[e + 2], wp[e + 3]);
+    }
     // lane (l16, q4) holds, per block i, row 16 i + l16 at columns
     // 64 hh + 16 q4 + [0, 16): partial dots, then a 4-lane butterfly over q4;
     // one half (hh) of the columns at a time: 16 values of T0 in registers
@@ -661,8 +709,16 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
         tot = R2[0] + __shfl_xor(R2[0], 32);
         row = 16 * (q4 & 1) + l16;
       }
-      const float sc = f16_bits_to_f32((uint16_t)sc_bits[NVB > 1 ? (row >> 5) : 0]);
-      if (NBLK >= 4 || q4 < 2) Act::st(out_rows, row, fmaf(tot, sc, wv_head[row]) * a.out_scale);
+      // scale of the row's vblock: row >> 5 = 2 m + (lane >> 5) (NBLK >= 4), else 0
+      // (a bit-select: a plain select of the two entries is folded back into a
+      // lane-indexed load from a private array)
+      uint32_t sb = sc_bits[NBLK >= 4 ? 2 * m : 0];
+      if constexpr (NBLK >= 4) sb ^= (sb ^ sc_bits[2 * m + 1]) & (0u - (uint32_t)(lane >> 5));
+      const float sc = f16_bits_to_f32((uint16_t)sb);
+      float wrow = 0.f;
+#pragma unroll
+      for (int mm = 0; mm < 64 / CPT_V; ++mm) wrow += part[(row / EPC + CPT_V * mm) * EPC + row % EPC];
+      if (NBLK >= 4 || q4 < 2) Act::st(out_rows, row, fmaf(tot, sc, wrow) * a.out_scale);
     }
     append_token();
     return;
@@ -689,14 +745,19 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
     const float lam_all = ((const float*)(lds + a.lds_lam))[j_head];
     uint4* ubuf = (uint4*)(lds + a.lds_u + j_head * LP * 192);  // U~^T: [block mm][lane]
     float4* wbuf = (float4*)(ubuf + 2 * 64);                   // W^T:  [lane]
-    // codes of vblock p: cf[hh * 2 + mm] (the layout of ck), next vblock prefetched
+    // codes of vblock p: cf[hh * 2 + mm] (the layout of ck), next vblock
+    // prefetched. The row pointer is laundered: the compiler must not fold
+    // these loads into the replay's ck registers (that would keep all of ck
+    // live through the rebuild).
     uint4 cf[4], cn[4];
+    const uint8_t* ck_rows_f = ck_rows;
+    asm volatile("" : "+s"(ck_rows_f));
     auto load_vb = [&](int p, uint4* d) {
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
         for (int mm = 0; mm < 2; ++mm)
-          d[hh * 2 + mm] = *(const uint4*)(ck_rows + ((32 * p + 16 * mm) * a.ck_v + 64 * hh + ck_lo));
+          d[hh * 2 + mm] = *(const uint4*)(ck_rows_f + ((32 * p + 16 * mm) * a.ck_v + 64 * hh + ck_lo));
     };
     load_vb(0, cf);
 #pragma unroll 1

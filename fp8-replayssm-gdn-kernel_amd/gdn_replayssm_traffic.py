@@ -110,3 +110,94 @@ def reference_traffic(s: LayerShape, window: int, block_v: int) -> dict:
         "flush_actual": 2 * checkpoint + 2 * scales + tiles * ring_key + ring_value + ring_scalars,
         "bf16_baseline": bf16_rmw_bytes(s),
     }
+
+
+# ---------------------------------------------------------------------------
+# Measured traffic: rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE reduction
+# ---------------------------------------------------------------------------
+
+def _counter_rows(run_dir):
+    """(dispatch_id, kernel_name, counter_name, value) of every
+    *counter_collection.csv under ``run_dir`` (rocprofv3 --output-format csv)."""
+    import csv
+    from pathlib import Path
+
+    files = sorted(Path(run_dir).rglob("*counter_collection.csv"))
+    if not files:
+        raise FileNotFoundError(f"no *counter_collection.csv under {run_dir}")
+    rows = []
+    for f in files:
+        with open(f, newline="") as fh:
+            for r in csv.DictReader(fh):
+                rows.append((int(r["Dispatch_Id"]), r["Kernel_Name"], r["Counter_Name"], float(r["Counter_Value"])))
+    return rows
+
+
+def _per_dispatch(rows, counter):
+    """Counter value per dispatch (summed over the dimensions rocprofv3 reports)."""
+    out = {}
+    names = {}
+    for dispatch, name, cname, value in rows:
+        if cname != counter:
+            continue
+        out[dispatch] = out.get(dispatch, 0.0) + value
+        names[dispatch] = name
+    return out, names
+
+
+def reduce_pmc(fetch_dir, write_dir, kernel: str, calib_bytes: int, calib_copies: int) -> dict:
+    """HBM bytes per launch of ``kernel`` from two rocprofv3 --pmc runs of the
+    same command (FETCH_SIZE, then WRITE_SIZE; KiB per dispatch). The command
+    ends with ``calib_copies`` plain device copies of ``calib_bytes`` bytes;
+    those last dispatches calibrate each counter (bytes the copy must move /
+    KiB the counter reports), and the kernel's mean KiB per dispatch is scaled
+    by that factor."""
+    result = {"kernel": kernel, "calibration": {"copy_bytes": calib_bytes, "copies": calib_copies}}
+    total = 0.0
+    for label, run_dir, counter in (("fetch", fetch_dir, "FETCH_SIZE"), ("write", write_dir, "WRITE_SIZE")):
+        values, names = _per_dispatch(_counter_rows(run_dir), counter)
+        order = sorted(values)
+        calib = order[-calib_copies:]
+        calib_kib = sum(values[d] for d in calib) / len(calib)
+        factor = calib_bytes / (calib_kib * 1024.0)
+        launches = [d for d in order if kernel in names[d]]
+        if not launches:
+            raise ValueError(f"no dispatch of {kernel!r} in {run_dir}")
+        kib = sum(values[d] for d in launches) / len(launches)
+        by_bytes = kib * 1024.0 * factor
+        total += by_bytes
+        result[label] = {
+            "counter": counter,
+            "kernel_dispatches": len(launches),
+            "kernel_kib_per_dispatch": kib,
+            "copy_kernel": names[calib[0]],
+            "copy_kib_per_dispatch": calib_kib,
+            "factor": factor,
+            "bytes_per_launch": by_bytes,
+        }
+    result["bytes_per_launch"] = total
+    return result
+
+
+if __name__ == "__main__":
+    import argparse
+    import json
+
+    p = argparse.ArgumentParser(description="Reduce rocprofv3 FETCH_SIZE / WRITE_SIZE runs to HBM bytes per launch")
+    p.add_argument("--fetch", required=True, help="rocprofv3 -d directory of the FETCH_SIZE run")
+    p.add_argument("--write", required=True, help="rocprofv3 -d directory of the WRITE_SIZE run")
+    p.add_argument("--kernel", default="step_kernel", help="substring of the kernel name")
+    p.add_argument("--calib-bytes", type=int, default=64 << 20)
+    p.add_argument("--calib-copies", type=int, default=4)
+    p.add_argument("--algorithmic-bytes", type=float, default=None,
+                   help="algorithmic bytes per launch, recorded beside the measured figure")
+    p.add_argument("--out", required=True)
+    args = p.parse_args()
+    res = reduce_pmc(args.fetch, args.write, args.kernel, args.calib_bytes, args.calib_copies)
+    if args.algorithmic_bytes:
+        res["algorithmic_bytes_per_launch"] = args.algorithmic_bytes
+        res["traffic_over_algorithmic"] = res["bytes_per_launch"] / args.algorithmic_bytes
+    with open(args.out, "w") as fh:
+        json.dump(res, fh, indent=1)
+        fh.write("\n")
+    print(json.dumps(res, indent=1))
