@@ -224,8 +224,8 @@ int fit_lds(gdnr::ReplayArgs* a, int es, bool stage_k, bool stage_v) {
 }
 
 // LDS plan of the step kernel (gdnr_step.hip, L <= kStepRing) for the
-// current gw / block_v: q | new k | k ring | flags | w | T0 | slot Gram per head |
-// v rows | flush: R | factors | K^T tiles | lam_all | U~/W tiles.
+// current gw / block_v: q | new k | k ring | flags | c | T0 | slot Gram per head |
+// v rows | flush: R | factors | K^T tiles | lam_all | U~/W tiles (two waves a head).
 int32_t layout_step(gdnr::ReplayArgs* a, int es) {
   const int64_t K = gdnr::kKeyDim, LP = gdnr::kStepRing;
   a->rpw = a->block_v;  // one streamer wave per head owns the head's block_v rows
@@ -239,7 +239,7 @@ int32_t layout_step(gdnr::ReplayArgs* a, int es) {
   region(&a->lds_knew, K * es);
   region(&a->lds_k, (int64_t)a->L * K * es);
   region(&a->lds_flag, (int64_t)a->gw * 20);  // 3 flags + new (gamma, beta) per head
-  region(&a->lds_c, (int64_t)a->gw * a->block_v * 4);  // w = sum_t c_t v_t per row
+  region(&a->lds_c, (int64_t)a->gw * a->block_v * 4);  // c_t per head (replay)
   region(&a->lds_t, (int64_t)a->gw * K * 4);
   region(&a->lds_g, (int64_t)a->gw * (LP + 2) * 20 * 4);  // [slots, q, new k]^2, row stride 20
   region(&a->lds_v, (int64_t)a->gw * LP * a->rpw * es);
@@ -247,7 +247,7 @@ int32_t layout_step(gdnr::ReplayArgs* a, int es) {
   region(&a->lds_fac, (int64_t)a->gw * LP * 16);
   region(&a->lds_kt, K * LP * es);
   region(&a->lds_lam, (int64_t)a->gw * 4);
-  region(&a->lds_u, (int64_t)a->gw * LP * 192);
+  region(&a->lds_u, (int64_t)2 * a->gw * LP * 192);  // U~/W scratch per flushing wave
   a->lds_bytes = (int32_t)off;
   return a->lds_bytes;
 }

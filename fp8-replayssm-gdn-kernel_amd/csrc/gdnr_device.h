@@ -159,6 +159,38 @@ __device__ __forceinline__ uint32_t f32x4_to_fp8(float a, float b, float c, floa
 __device__ __forceinline__ float clamp448(float x) {
   return (x != x) ? x : fminf(fmaxf(x, -448.0f), 448.0f);
 }
+// 4 floats -> 4 codes exactly as the reference's clamp + e4m3fn cast writes
+// them, for any input: clamp to +-448 keeping NaN, round to nearest even, NaN
+// -> 0x7F | sign (the convert instruction writes 0xFF for every NaN).
+__device__ __forceinline__ uint32_t f32x4_to_fp8_ref(float a, float b, float c, float d) {
+  uint32_t w = f32x4_to_fp8(clamp448(a), clamp448(b), clamp448(c), clamp448(d));
+  const float v[4] = {a, b, c, d};
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    if (v[e] != v[e]) w = (w & ~(0xFFu << (8 * e))) | ((__float_as_uint(v[e]) >> 31 ? 0xFFu : 0x7Fu) << (8 * e));
+  return w;
+}
+
+// Quantiser quotient: the correctly rounded x / s (what IEEE division gives)
+// from r = RN(1/s), in 5 VALU operations instead of the division sequence.
+// q0 = RN(x r) is within 1.5 ulp of x / s; a correction with the residual
+// x - s q (exact by FMA) brings it within 1 ulp, and a second correction is
+// correctly rounded (Markstein's theorem: r within 1/2 ulp of 1/s, q within
+// 1 ulp of x / s, no underflow or overflow). Callers use it only when the
+// block's amax is finite and s >= 2^-64, so |x / s| <= 448 (1 + 2^-23) and
+// every quotient the fp8 code depends on (|x / s| >= 2^-10) is a normal
+// number; the corrections turn -0 into +0, so the sign is restored.
+__device__ __forceinline__ float quotient_rn(float x, float s, float r) {
+  float q = x * r;
+  q = fmaf(fmaf(-q, s, x), r, q);
+  q = fmaf(fmaf(-q, s, x), r, q);
+  return __builtin_copysignf(q, x);
+}
+// Whether a block with this amax (bits of |x| max) and scale takes quotient_rn:
+// amax finite and s >= 2^-64.
+__device__ __forceinline__ bool quotient_fast(uint32_t amax_bits, float s) {
+  return amax_bits < 0x7F800000u && s >= 0x1p-64f;
+}
 
 // ---------------------------------------------------------------- cross-lane (DPP, wave64)
 template <int CTRL, int ROW_MASK = 0xF>

@@ -440,13 +440,22 @@ __global__ __launch_bounds__(256) void replay_kernel(const ReplayArgs a) {
       const float amax = __uint_as_float(am);
       const float s32 = (amax > 0.0f) ? amax / 448.0f : 1.0f;
       const _Float16 s16 = (_Float16)s32;
+      const bool fast = quotient_fast(am, s32);
+      const float r = 1.0f / s32;
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) {
         uint32_t wq[4];
+        if (fast) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          wq[i] = f32x4_to_fp8(clamp448(s[jj][4 * i] / s32), clamp448(s[jj][4 * i + 1] / s32),
-                               clamp448(s[jj][4 * i + 2] / s32), clamp448(s[jj][4 * i + 3] / s32));
+          for (int i = 0; i < 4; ++i)
+            wq[i] = f32x4_to_fp8(quotient_rn(s[jj][4 * i], s32, r), quotient_rn(s[jj][4 * i + 1], s32, r),
+                                 quotient_rn(s[jj][4 * i + 2], s32, r), quotient_rn(s[jj][4 * i + 3], s32, r));
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            wq[i] = f32x4_to_fp8_ref(s[jj][4 * i] / s32, s[jj][4 * i + 1] / s32, s[jj][4 * i + 2] / s32,
+                                     s[jj][4 * i + 3] / s32);
+        }
         *(uint4*)(ckp + (int64_t)(8 * (4 * p + jj)) * a.ck_v) = make_uint4(wq[0], wq[1], wq[2], wq[3]);
       }
       if (lane == 0)
@@ -588,20 +597,36 @@ __global__ __launch_bounds__(256) void quantize_kernel(const QuantArgs a) {
   const float s32 = (amax > 0.0f) ? amax / 448.0f : 1.0f;
   int sat = 0;
   uint8_t* dst = a.codes + (int64_t)b * a.ck_b + (int64_t)hv * a.ck_h + (int64_t)(vb * kVBlock + gm) * a.ck_v + 16 * gi;
+  // quotients x / s32 as IEEE division rounds them: quotient_rn when the
+  // block is finite (|x / s32| <= 448 (1 + 2^-23): no clamp needed), else
+  // the division with the reference's clamp and NaN encoding
+  const bool fast = quotient_fast(am, s32);
+  const float r = 1.0f / s32;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     float y[16];
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      y[e] = x[j][e] / s32;
-      sat += fabsf(y[e]) > 448.0f ? 1 : 0;
-      y[e] = clamp448(y[e]);
-    }
     uint4 w;
-    w.x = f32x4_to_fp8(y[0], y[1], y[2], y[3]);
-    w.y = f32x4_to_fp8(y[4], y[5], y[6], y[7]);
-    w.z = f32x4_to_fp8(y[8], y[9], y[10], y[11]);
-    w.w = f32x4_to_fp8(y[12], y[13], y[14], y[15]);
+    if (fast) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        y[e] = quotient_rn(x[j][e], s32, r);
+        sat += fabsf(y[e]) > 448.0f ? 1 : 0;
+      }
+      w.x = f32x4_to_fp8(y[0], y[1], y[2], y[3]);
+      w.y = f32x4_to_fp8(y[4], y[5], y[6], y[7]);
+      w.z = f32x4_to_fp8(y[8], y[9], y[10], y[11]);
+      w.w = f32x4_to_fp8(y[12], y[13], y[14], y[15]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        y[e] = x[j][e] / s32;
+        sat += fabsf(y[e]) > 448.0f ? 1 : 0;
+      }
+      w.x = f32x4_to_fp8_ref(y[0], y[1], y[2], y[3]);
+      w.y = f32x4_to_fp8_ref(y[4], y[5], y[6], y[7]);
+      w.z = f32x4_to_fp8_ref(y[8], y[9], y[10], y[11]);
+      w.w = f32x4_to_fp8_ref(y[12], y[13], y[14], y[15]);
+    }
     *(uint4*)(dst + (int64_t)(8 * j) * a.ck_v) = w;
   }
   sat = wave_sum_i32(sat);

@@ -101,6 +101,9 @@ __device__ __forceinline__ float row_suffix_prod(float x) {
   return x;
 }
 
+// the workgroup's dynamic LDS (layout in StepArgs: lds_* byte offsets)
+extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+
 // byte offset of byte `by` of token t's row in the swizzled k ring (ROWB = K * ES)
 template <int ROWB>
 __device__ __forceinline__ int kr_off(int t, int by) {
@@ -142,9 +145,285 @@ __device__ __forceinline__ float gate_value(uint32_t bits) {
   else return Act::from_bits(bits);
 }
 
+// ---- flush (section 7), out of line: the rebuild's register pressure stays
+// out of the replay path's allocation. Every operand is wave-uniform; the
+// call passes them one by one in VGPRs (a struct would go through the stack),
+// so they are made uniform again on entry.
+struct FlushArgs {
+  uint8_t* ck_rows;   // the head's checkpoint rows (block_v rows of ck_v bytes)
+  uint8_t* scale_hv;  // the head's vblock scales
+  uint8_t* out_rows;  // the head's output rows
+  uint32_t ck_v, sc_v;  // row / vblock byte strides
+  int32_t sc_row0;      // first vblock of the rows
+  float out_scale;
+  int32_t lds_k, lds_knew, lds_q, lds_r, lds_fac, lds_lam, lds_kt, vbuf, uoff;
+  int32_t j_head, n, pos, fp0, fp1;  // head, ring fill, new slot, vblocks [fp0, fp1)
+};
+
+__device__ __forceinline__ int32_t uni(int32_t x) { return __builtin_amdgcn_readfirstlane(x); }
+// global-memory view of a pointer passed as a generic one (the callee would
+// otherwise access it with flat instructions, which count in both wait counters)
+template <class T>
+__device__ __forceinline__ __attribute__((address_space(1))) T* gptr(const void* p) {
+  return (__attribute__((address_space(1))) T*)p;
+}
+__device__ __forceinline__ uint8_t* uni(uint8_t* p) {
+  const uint64_t v = (uint64_t)p;
+  return (uint8_t*)(((uint64_t)(uint32_t)uni((int32_t)(v >> 32)) << 32) | (uint32_t)uni((int32_t)v));
+}
+
+template <class Act, int NCH>
+__device__ __attribute__((noinline)) void flush_vblocks(
+    uint8_t* f_ck_rows, uint8_t* f_scale_hv, uint8_t* f_out_rows, uint32_t f_ck_v, uint32_t f_sc_v, int32_t f_sc_row0,
+    float f_out_scale, int32_t f_lds_k, int32_t f_lds_knew, int32_t f_lds_q, int32_t f_lds_r, int32_t f_lds_fac,
+    int32_t f_lds_lam, int32_t f_lds_kt, int32_t f_vbuf, int32_t f_uoff, int32_t f_j_head, int32_t f_n, int32_t f_pos,
+    int32_t f_fp0, int32_t f_fp1) {
+  FlushArgs f{f_ck_rows, f_scale_hv, f_out_rows, f_ck_v, f_sc_v, f_sc_row0, f_out_scale, f_lds_k, f_lds_knew, f_lds_q,
+              f_lds_r, f_lds_fac, f_lds_lam, f_lds_kt, f_vbuf, f_uoff, f_j_head, f_n, f_pos, f_fp0, f_fp1};
+  constexpr int ES = Act::kBytes;
+  constexpr int ROWB = K * ES;
+  constexpr int RPW = 8 * NCH;
+  constexpr bool BF16 = std::is_same<Act, ActBF16>::value;
+  constexpr bool F16 = std::is_same<Act, ActF16>::value;
+  const int lane = threadIdx.x & 63;
+  const int q4 = lane >> 4, l16 = lane & 15;
+  const int j_head = uni(f.j_head), n = uni(f.n), pos = uni(f.pos), fp0 = uni(f.fp0), fp1 = uni(f.fp1);
+  const int uoff = uni(f.uoff);
+  const uint32_t ck_v = (uint32_t)uni((int32_t)f.ck_v), sc_v = (uint32_t)uni((int32_t)f.sc_v);
+  f.sc_row0 = uni(f.sc_row0), f.lds_k = uni(f.lds_k), f.lds_knew = uni(f.lds_knew), f.lds_q = uni(f.lds_q);
+  f.lds_r = uni(f.lds_r), f.lds_fac = uni(f.lds_fac), f.lds_lam = uni(f.lds_lam), f.lds_kt = uni(f.lds_kt);
+  f.out_scale = __builtin_bit_cast(float, uni(__builtin_bit_cast(int32_t, f.out_scale)));
+  uint8_t* ck_rows = uni(f.ck_rows);
+  uint8_t* scale_hv = uni(f.scale_hv);
+  uint8_t* out_rows = uni(f.out_rows);
+  const uint8_t* vbuf = lds + uni(f.vbuf);
+  const uint32_t ck_lo = (uint32_t)l16 * ck_v + 16 * q4;
+  const XRows xr{f.lds_k, f.lds_knew, f.lds_q, n, pos};
+  // Per vblock p (32 rows = 16-row blocks 2p, 2p + 1) lane l owns row l % 16
+  // of a block; the contraction walks the columns in the order of ck, so every
+  // checkpoint operand comes straight from those registers and the
+  // requantised codes go back as the same two 16-byte words.
+  //   A.  P^T = [K; q] S_0^T          (tokens x rows; the q row gives S_0 q)
+  //       W^T = v - pre . P^T
+  //   B.  U^T = R W^T,  U~^T = post . U^T,  o = lam_all S_0 q + sum_t U~^T[t] (k_t . q)
+  //   C.  S_n^T = lam_all S_0^T + K^T U~^T, two passes over the vblock:
+  //       amax, then requantisation.
+  // W^T and U~^T tiles are parked in this wave's LDS area in the MFMA
+  // B-operand layout ([tile][lane], 16 bytes a lane).
+  {
+    const int ntbx = n < LP ? 1 : 2;  // token blocks including the q row at index n
+    const float* Rj = (const float*)(lds + f.lds_r) + j_head * LP * LP;
+    const float4* fac = (const float4*)(lds + f.lds_fac) + j_head * LP;
+    const float lam_all = ((const float*)(lds + f.lds_lam))[j_head];
+    uint4* ubuf = (uint4*)(lds + uoff);  // U~^T: [block mm][lane]
+    float4* wbuf = (float4*)(ubuf + 2 * 64);                   // W^T:  [lane]
+    // codes of vblock p: cf[hh * 2 + mm] (the layout of ck); the next
+    // vblock's are requested into the same registers as soon as the rebuild
+    // has consumed them. The row pointer is laundered: the compiler must not
+    // fold these loads into the replay's ck registers (that would keep all of
+    // ck live through the rebuild).
+    uint4 cf[4];
+    const uint8_t* ck_rows_f = ck_rows;
+    asm volatile("" : "+s"(ck_rows_f));
+    auto load_vb = [&](int p, uint4* d) {
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+        for (int mm = 0; mm < 2; ++mm)
+        {
+          const u32x4_t w = *gptr<const u32x4_t>(ck_rows_f + ((32 * p + 16 * mm) * ck_v + 64 * hh + ck_lo));
+          d[hh * 2 + mm] = make_uint4(w[0], w[1], w[2], w[3]);
+        }
+    };
+    if (fp0 < fp1) load_vb(fp0, cf);
+#pragma unroll 1
+    for (int p = fp0; p < fp1; ++p) {
+      const float sc = f16_bits_to_f32((uint16_t)ld_u16_uniform((const uint16_t*)(scale_hv + (f.sc_row0 + p) * sc_v)));
+#pragma unroll
+      for (int mm = 0; mm < 2; ++mm) {
+        const int blk = 2 * p + mm;
+        const int rl = 16 * blk + l16;  // row within this wave's rows
+        const uint4 c0 = cf[mm], c1 = cf[2 + mm];
+        const uint32_t cw[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+        float o_part = 0.f;
+        // A: P^T blocks and W^T
+#pragma unroll 1
+        for (int tb = 0; tb < ntbx; ++tb) {
+          const int x = tb * 16 + l16;  // token row of X supplied by this lane
+          const bool zero_x = x > n;
+          f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+          if constexpr (BF16 || F16) {
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+              // columns 64 (m / 2) + 16 q4 + 8 (m % 2) + [0, 8): words 2m, 2m + 1
+              uint4 av = *(const uint4*)(lds + xr.off<ROWB>(x, (64 * (m >> 1) + 16 * q4 + 8 * (m & 1)) * 2));
+              if (zero_x) av = make_uint4(0u, 0u, 0u, 0u);
+              float f[8];
+              fp8x4_to_f32(opaque(cw[2 * m]), f);
+              fp8x4_to_f32(opaque(cw[2 * m + 1]), f + 4);
+              if constexpr (BF16) {
+                // e4m3 values are exact in bf16
+                const uint4 bv = make_uint4(pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]), pack_bf16x2(f[4], f[5]),
+                                            pack_bf16x2(f[6], f[7]));
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, av),
+                                                              __builtin_bit_cast(bf16x8_t, bv), acc, 0, 0, 0);
+              } else {
+                const f16x8_t bv = {(_Float16)f[0], (_Float16)f[1], (_Float16)f[2], (_Float16)f[3],
+                                    (_Float16)f[4], (_Float16)f[5], (_Float16)f[6], (_Float16)f[7]};
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, av), bv, acc, 0, 0, 0);
+              }
+            }
+          } else {
+#pragma unroll
+            for (int kc = 0; kc < 8; ++kc) {
+              const int col = 64 * (kc >> 2) + 16 * q4 + 4 * (kc & 3);
+              float f[4];
+              fp8x4_to_f32(opaque(cw[kc]), f);
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                float av = *(const float*)(lds + xr.off<ROWB>(x, (col + e) * 4));
+                av = zero_x ? 0.f : av;
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av, f[e], acc, 0, 0, 0);
+              }
+            }
+          }
+          float wv[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int t = tb * 16 + 4 * q4 + e;
+            const float pv = acc[e] * sc;
+            if (t < n) {
+              wv[e] = Act::ld(vbuf, t * RPW + rl) - fac[t].x * pv;
+            } else {
+              wv[e] = 0.f;
+              if (t == n) o_part = fmaf(lam_all, pv, o_part);
+            }
+          }
+          // the block holding only the q row (tb == 1) is not a token block of W^T
+          if (tb == 0) wbuf[lane] = make_float4(wv[0], wv[1], wv[2], wv[3]);
+        }
+        // B: U^T = R W^T (fp32 MFMA, contraction index q4 <-> token 4 q4 + e)
+        {
+          f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+          const float4 wv = wbuf[lane];
+          const float* rrow = Rj + l16 * LP + 4 * q4;
+          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(rrow[0], wv.x, acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(rrow[1], wv.y, acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(rrow[2], wv.z, acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(rrow[3], wv.w, acc, 0, 0, 0);
+          float ut[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float4 f = fac[4 * q4 + e];
+            ut[e] = acc[e] * f.y;
+            o_part = fmaf(ut[e], f.z, o_part);
+          }
+          uint4 packed;
+          if constexpr (BF16) {
+            // hi/lo split: U~ = hi + lo to ~16 bits, both halves bf16 MFMA operands
+            const uint32_t h01 = pack_bf16x2(ut[0], ut[1]), h23 = pack_bf16x2(ut[2], ut[3]);
+            const uint32_t l01 =
+                pack_bf16x2(ut[0] - __uint_as_float(h01 << 16), ut[1] - __uint_as_float(h01 & 0xFFFF0000u));
+            const uint32_t l23 =
+                pack_bf16x2(ut[2] - __uint_as_float(h23 << 16), ut[3] - __uint_as_float(h23 & 0xFFFF0000u));
+            packed = make_uint4(h01, h23, l01, l23);
+          } else {
+            packed = make_uint4(__float_as_uint(ut[0]), __float_as_uint(ut[1]), __float_as_uint(ut[2]),
+                                __float_as_uint(ut[3]));
+          }
+          ubuf[mm * 64 + lane] = packed;
+        }
+        o_part += __shfl_xor(o_part, 16);
+        o_part += __shfl_xor(o_part, 32);
+        if (q4 == 0) {
+          const float o = o_part * f.out_scale;
+          if constexpr (ES == 4) *gptr<float>(out_rows + 4 * rl) = o;
+          else if constexpr (BF16) *gptr<uint16_t>(out_rows + 2 * rl) = (uint16_t)f32_to_bf16(o);
+          else *gptr<_Float16>(out_rows + 2 * rl) = (_Float16)o;
+        }
+      }
+      // C: S_n^T tiles sn[mm][ct] of block mm (ct = 4 hh + w): D row 4 q4 + e
+      // of tile ct is column 64 hh + 16 q4 + 4 w + e, and row l16 of K^T tile
+      // ct (the A operand of lane l) holds that column ordering already. Both
+      // blocks of the vblock stay in registers for the amax and the
+      // requantisation (the reference quantiser, ref:36-37,83-99: s =
+      // amax/448, 1 when amax is not > 0; codes = e4m3fn(clamp(x / s, +-448))
+      // with the unrounded fp32 s; the quotient by quotient_rn when the block
+      // is finite).
+      f32x4_t sn[2][8];
+      uint32_t am = 0;
+#pragma unroll
+      for (int mm = 0; mm < 2; ++mm) {
+#pragma unroll
+        for (int ct = 0; ct < 8; ++ct) {
+          const uint4 c = cf[(ct >> 2) * 2 + mm];
+          const uint32_t wd = (ct & 3) == 0 ? c.x : (ct & 3) == 1 ? c.y : (ct & 3) == 2 ? c.z : c.w;
+          float f[4];
+          fp8x4_to_f32(wd, f);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) sn[mm][ct][e] = lam_all * (f[e] * sc);
+        }
+        if (mm == 1 && p + 1 < fp1) load_vb(p + 1, cf);  // the codes of vblock p are consumed
+        const uint4 u = ubuf[mm * 64 + lane];
+        const uint8_t* kt_lane = lds + f.lds_kt + l16 * 16 * ES + 4 * q4 * ES;  // tokens 4 q4 + e
+#pragma unroll
+        for (int ct = 0; ct < 8; ++ct) {
+          const uint8_t* ktrow = kt_lane + ct * 256 * ES;
+          if constexpr (BF16) {
+            const bf16x4_t av = __builtin_bit_cast(bf16x4_t, *(const uint2*)ktrow);
+            sn[mm][ct] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(av, __builtin_bit_cast(bf16x4_t, make_uint2(u.x, u.y)),
+                                                                   sn[mm][ct], 0, 0, 0);
+            sn[mm][ct] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(av, __builtin_bit_cast(bf16x4_t, make_uint2(u.z, u.w)),
+                                                                   sn[mm][ct], 0, 0, 0);
+          } else {
+            const float uf[4] = {__uint_as_float(u.x), __uint_as_float(u.y), __uint_as_float(u.z),
+                                 __uint_as_float(u.w)};
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              sn[mm][ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(Act::ld(ktrow, e), uf[e], sn[mm][ct], 0, 0, 0);
+          }
+        }
+#pragma unroll
+        for (int ct = 0; ct < 8; ++ct)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) am = max(am, __float_as_uint(sn[mm][ct][e]) & 0x7FFFFFFFu);
+      }
+      const uint32_t amb = wave_max_u32(am);
+      const float amax = __uint_as_float(amb);
+      const float s32 = (amax > 0.0f) ? amax / 448.0f : 1.0f;
+      const bool fast = quotient_fast(amb, s32);
+      const float rcp = 1.0f / s32;
+#pragma unroll
+      for (int mm = 0; mm < 2; ++mm) {
+        uint8_t* rp = ck_rows + ((16 * (2 * p + mm) + l16) * ck_v + 16 * q4);
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          uint32_t wd[4];
+          if (fast) {
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+              const f32x4_t& v = sn[mm][4 * hh + w];
+              wd[w] = f32x4_to_fp8(quotient_rn(v[0], s32, rcp), quotient_rn(v[1], s32, rcp),
+                                   quotient_rn(v[2], s32, rcp), quotient_rn(v[3], s32, rcp));
+            }
+          } else {
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+              const f32x4_t& v = sn[mm][4 * hh + w];
+              wd[w] = f32x4_to_fp8_ref(v[0] / s32, v[1] / s32, v[2] / s32, v[3] / s32);
+            }
+          }
+          *gptr<u32x4_t>(rp + 64 * hh) = u32x4_t{wd[0], wd[1], wd[2], wd[3]};
+        }
+      }
+      if (lane == 0)
+        *gptr<uint16_t>(scale_hv + (f.sc_row0 + p) * sc_v) = __builtin_bit_cast(uint16_t, (_Float16)s32);
+    }
+  }
+}
+
 template <class Act, int NCH, bool FUSED, bool GATE_F32>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void step_kernel(const StepArgs a) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   constexpr int ES = Act::kBytes;
   constexpr int ROWB = K * ES;          // bytes of one k-ring row
   constexpr int RPW = 8 * NCH;          // V-rows per streamer (= block_v)
@@ -177,10 +456,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
 
   // ---- 0. the head leads publish their coefficients through LDS flags -------------
   // flags[j]: head j's coefficients are in LDS; flags[gw + j]: lead j's
-  // share of the k ring has landed; then the new token's (gamma, beta) per head
+  // share of the k ring has landed; flags[2 gw + j]: streamer j's copy of
+  // the v rows is in LDS; then the new token's (gamma, beta) per head
   int* flags = (int*)(lds + a.lds_flag);
-  float* newgates = (float*)(flags + 2 * a.gw);
-  if (wave == 0 && lane < 2 * a.gw) flags[lane] = 0;
+  float* newgates = (float*)(flags + 3 * a.gw);
+  if (wave == 0 && lane < 3 * a.gw) flags[lane] = 0;
   GDNR_WAIT_LGKM0();
   __builtin_amdgcn_s_barrier();  // B0, the only workgroup barrier
 
@@ -223,6 +503,53 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
   // w = sum_t c_t v_t (replay) or stages them in LDS (flush).
   uint8_t* vbuf = lds + a.lds_v + j_head * LP * RPW * ES;
   float* c_head = (float*)(lds + a.lds_c) + j_head * RPW;  // c_t of head j (replay)
+  // checkpoint rows (replay): ck[hh * NBLK + i] = row 16 i + l16, bytes
+  // [64 hh + 16 q4, +16); word w of it holds columns 64 hh + 16 q4 + 4 w + e,
+  // at a uniform base per 16-row block + one 32-bit lane offset
+  uint8_t* scale_hv = a.scale + (b * a.sc_b + hv * a.sc_h);
+  uint8_t* ck_rows = a.ckpt + (b * a.ck_b + hv * a.ck_h + (v0 + r0) * a.ck_v);
+  const uint32_t ck_lo = (uint32_t)l16 * a.ck_v + 16 * q4;
+  uint8_t* out_rows = a.out + (b * a.o_b + hv * a.o_h + (v0 + r0) * ES);
+  // wait for this head's lead (bounded: the lead always publishes)
+  auto await_coefficients = [&]() {
+    for (int it = 0; it < (1 << 22); ++it) {
+      if (flag_set(flags + j_head)) break;
+      __builtin_amdgcn_s_sleep(1);
+    }
+  };
+  // Ring append of the new token (full contract): its v rows from this
+  // wave's LDS copy, its gates, and (streamer 0 of the key head's first
+  // workgroup) q (output) and k from what the lead left in LDS. Issued after
+  // every load of the wave.
+  auto append_token = [&]() {
+    if constexpr (FUSED) {
+      if (pos >= 0) {
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+          const int c = 64 * i + lane;
+          if (c / CPT_V == pos)
+            *(u32x4_t*)(a.v + (b * a.v_b + pos * a.v_t + hv * a.v_h + v0 * ES + 16 * (c % CPT_V))) =
+                *(const u32x4_t*)(vbuf + 16 * c);
+        }
+        if (vt == 0 && lane == 0) {
+          Act::st(a.g + (b * a.g_b + pos * a.g_t + hv * a.g_h), 0, newgates[2 * j_head]);
+          Act::st(a.beta + (b * a.be_b + pos * a.be_t + hv * a.be_h), 0, newgates[2 * j_head + 1]);
+        }
+      }
+      if (j_head == 0 && vt == 0 && sub == 0) {
+        const float2 q2 = Act::ld2(lds + a.lds_q + 2 * lane * ES);
+        Act::st2(a.q_out + (b * a.qo_b + h * a.qo_h + 2 * lane * ES), q2.x, q2.y);
+        if (pos >= 0) {
+          const float2 k2 = Act::ld2(lds + a.lds_knew + 2 * lane * ES);
+          Act::st2(a.k + (b * a.k_b + pos * a.k_t + h * a.k_h + 2 * lane * ES), k2.x, k2.y);
+        }
+      }
+    }
+  };
+
+  // vblocks [fp0, fp1) of the head that this wave rebuilds in a flush, and its
+  // U~/W scratch in LDS
+  int fp0 = 0, fp1 = 0, uoff = 0;
   if (__builtin_amdgcn_readfirstlane((int)head_lead) != 0) {
     const int j = j_head;
     typename Act::Pair q_bits{}, k_bits{};
@@ -512,430 +839,193 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
       newgates[2 * j] = gate_new;
       newgates[2 * j + 1] = beta_new;
     }
-    // publish: this head's coefficients, w (or flush factors), v rows, new
-    // gates and the shared q / new k / K^T are in LDS
+    // publish: this head's coefficients (or flush factors), new gates and
+    // the shared q / new k / K^T are in LDS
     __hip_atomic_store(flags + j, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
-    return;
+    if (__builtin_amdgcn_readfirstlane((int)do_flush) == 0) return;
+    // a flush splits the head's vblocks between the two waves of the head:
+    // the lead takes the upper half once the streamer's copy of the v rows
+    // is in LDS (bounded wait: the streamer always raises the flag)
+    for (int it = 0; it < (1 << 22); ++it) {
+      if (flag_set(flags + 2 * a.gw + j)) break;
+      __builtin_amdgcn_s_sleep(1);
+    }
+    fp0 = NVB / 2, fp1 = NVB, uoff = a.lds_u + (a.gw + j) * LP * 192;
   }
 
   // ---- streamer of head j_head ---------------------------------------------------
-  // checkpoint rows (replay): ck[hh * NBLK + i] = row 16 i + l16, bytes
-  // [64 hh + 16 q4, +16); word w of it holds columns 64 hh + 16 q4 + 4 w + e,
-  // at a uniform base per 16-row block + one 32-bit lane offset
-  uint8_t* scale_hv = a.scale + (b * a.sc_b + hv * a.sc_h);
-  uint8_t* ck_rows = a.ckpt + (b * a.ck_b + hv * a.ck_h + (v0 + r0) * a.ck_v);
-  const uint32_t ck_lo = (uint32_t)l16 * a.ck_v + 16 * q4;
-  uint8_t* out_rows = a.out + (b * a.o_b + hv * a.o_h + (v0 + r0) * ES);
-  // Stream once the k ring has landed (bounded waits: every lead raises its
-  // flag): the ring requests of the grid reach memory ahead of the checkpoint
-  // stream. A replay consumes the checkpoint rows from registers; a flush
-  // drops them and re-reads one vblock at a time in section 7 (its registers
-  // go to the rebuild instead).
-  for (int jj = 0; jj < a.gw; ++jj)
-    for (int it = 0; it < (1 << 22); ++it) {
-      if (flag_set(flags + a.gw + jj)) break;
-      __builtin_amdgcn_s_sleep(1);
-    }
-  read_meta();
-  // v rows of head j first (a replay folds them into w before its matvec):
-  // chunk c = 64 i + lane holds rows
-  // EPC (c % CPT_V) + [0, EPC) of token c / CPT_V. Tokens at or past the fill
-  // re-read slot 0 (a cache hit; dropped below); the new token's slot reads
-  // the new v from mixed_qkv. Every lane loads: the instruction count is static.
-  u32x4_t vch[NV];
-  {
-    const uint8_t* vring = a.v + (b * a.v_b + hv * a.v_h + v0 * ES);
-    const uint32_t vt_bytes = a.v_t;
-#pragma unroll
-    for (int i = 0; i < NV; ++i) {
-      const int c = 64 * i + lane;
-      const int t = c / CPT_V, rc = c % CPT_V;
-      const uint8_t* src = vring + ((uint32_t)(t < n ? t : 0) * vt_bytes + 16u * (uint32_t)rc);
-      if constexpr (FUSED)
-        if (t == pos) src = a.mixed + (b * a.mx_b + (2 * a.H * K + hv * a.V + v0) * ES + 16 * rc);
-      vch[i] = *(const u32x4_t*)src;
-    }
-  }
-  uint32_t sc_bits[NVB];  // scalar
-#pragma unroll
-  for (int p = 0; p < NVB; ++p) sc_bits[p] = ld_u16_uniform((const uint16_t*)(scale_hv + ((v0 + r0) / kVBlock + p) * a.sc_v));
-  uint4 ck[NCH];
-  GDNR_COMPILER_FENCE();
-  {
-    // one uniform base, a 32-bit lane offset per 16-row block
-    const uint32_t rstep = 16u * (uint32_t)a.ck_v;
-#pragma unroll
-    for (int i = 0; i < NBLK; ++i) {
-      const uint32_t off = ck_lo + (uint32_t)i * rstep;
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh) ck[hh * NBLK + i] = *(const uint4*)(ck_rows + (off + 64u * hh));
-    }
-  }
-  GDNR_COMPILER_FENCE();
-  // the v rows land ahead of the checkpoint rows: copy them to LDS in
-  // token-major order (chunk c at byte 16 c) and free their registers
-  GDNR_WAIT_VMCNT(NCH);
-#pragma unroll
-  for (int i = 0; i < NV; ++i) *(u32x4_t*)(vbuf + 16 * (64 * i + lane)) = vch[i];
-  // wait for this head's lead (bounded: the lead always publishes)
-  auto await_coefficients = [&]() {
-    for (int it = 0; it < (1 << 22); ++it) {
-      if (flag_set(flags + j_head)) break;
-      __builtin_amdgcn_s_sleep(1);
-    }
-  };
-  // Ring append of the new token (full contract): its v rows from this
-  // wave's LDS copy, its gates, and (streamer 0 of the key head's first
-  // workgroup) q (output) and k from what the lead left in LDS. Issued after
-  // every load of the wave.
-  auto append_token = [&]() {
-    if constexpr (FUSED) {
-      if (pos >= 0) {
-#pragma unroll
-        for (int i = 0; i < NV; ++i) {
-          const int c = 64 * i + lane;
-          if (c / CPT_V == pos)
-            *(u32x4_t*)(a.v + (b * a.v_b + pos * a.v_t + hv * a.v_h + v0 * ES + 16 * (c % CPT_V))) =
-                *(const u32x4_t*)(vbuf + 16 * c);
-        }
-        if (vt == 0 && lane == 0) {
-          Act::st(a.g + (b * a.g_b + pos * a.g_t + hv * a.g_h), 0, newgates[2 * j_head]);
-          Act::st(a.beta + (b * a.be_b + pos * a.be_t + hv * a.be_h), 0, newgates[2 * j_head + 1]);
-        }
+  if (__builtin_amdgcn_readfirstlane((int)head_lead) == 0) {
+    // Stream once the k ring has landed (bounded waits: every lead raises its
+    // flag): the ring requests of the grid reach memory ahead of the checkpoint
+    // stream. A replay holds its checkpoint rows in registers; a flush reads
+    // them one vblock at a time in section 7 (its registers go to the rebuild).
+    for (int jj = 0; jj < a.gw; ++jj)
+      for (int it = 0; it < (1 << 22); ++it) {
+        if (flag_set(flags + a.gw + jj)) break;
+        __builtin_amdgcn_s_sleep(1);
       }
-      if (j_head == 0 && vt == 0 && sub == 0) {
-        const float2 q2 = Act::ld2(lds + a.lds_q + 2 * lane * ES);
-        Act::st2(a.q_out + (b * a.qo_b + h * a.qo_h + 2 * lane * ES), q2.x, q2.y);
-        if (pos >= 0) {
-          const float2 k2 = Act::ld2(lds + a.lds_knew + 2 * lane * ES);
-          Act::st2(a.k + (b * a.k_b + pos * a.k_t + h * a.k_h + 2 * lane * ES), k2.x, k2.y);
-        }
-      }
-    }
-  };
-
-  // The replay and flush tails share no code after this point (each returns),
-  // so the checkpoint registers of the replay never meet the registers of the
-  // rebuild.
-  if (__builtin_amdgcn_readfirstlane((int)do_flush) == 0) {
-    // ---- replay: o = (scale * codes) . T0 + w -----------------------------------
-    await_coefficients();
-    // w = sum_t c_t v_t: per-lane partials over the lane's chunks (rows
-    // EPC rc + [0, EPC)), exchanged through LDS (this head's U~ area, unused
-    // by a replay) and summed per output row below
-    const float* part = (const float*)(lds + a.lds_u + j_head * LP * 192);  // [lane][EPC]
+    read_meta();
+    // v rows of head j first (a replay folds them into w before its matvec):
+    // chunk c = 64 i + lane holds rows
+    // EPC (c % CPT_V) + [0, EPC) of token c / CPT_V. Tokens at or past the fill
+    // re-read slot 0 (a cache hit; dropped below); the new token's slot reads
+    // the new v from mixed_qkv. Every lane loads: the instruction count is static.
+    u32x4_t vch[NV];
     {
-      float wp[EPC];
-#pragma unroll
-      for (int e = 0; e < EPC; ++e) wp[e] = 0.f;
+      const uint8_t* vring = a.v + (b * a.v_b + hv * a.v_h + v0 * ES);
+      const uint32_t vt_bytes = a.v_t;
 #pragma unroll
       for (int i = 0; i < NV; ++i) {
-        const int t = (64 * i + lane) / CPT_V;
-        const bool live = t < n;
-        const float ct = live ? c_head[live ? t : 0] : 0.f;
-        const u32x4_t vc = *(const u32x4_t*)(vbuf + 16 * (64 * i + lane));
-        const uint32_t wd[4] = {vc[0], vc[1], vc[2], vc[3]};
+        const int c = 64 * i + lane;
+        const int t = c / CPT_V, rc = c % CPT_V;
+        const uint8_t* src = vring + ((uint32_t)(t < n ? t : 0) * vt_bytes + 16u * (uint32_t)rc);
+        if constexpr (FUSED)
+          if (t == pos) src = a.mixed + (b * a.mx_b + (2 * a.H * K + hv * a.V + v0) * ES + 16 * rc);
+        vch[i] = *(const u32x4_t*)src;
+      }
+    }
+    if (__builtin_amdgcn_readfirstlane((int)do_flush) == 0) {
+      // ---- replay: o = (scale * codes) . T0 + w -----------------------------------
+      uint32_t sc_bits[NVB];  // scalar
 #pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          if constexpr (ES == 2) {
-            const float2 f = Act::from_pair(wd[w]);
-            wp[2 * w] = fmaf(ct, live ? f.x : 0.f, wp[2 * w]);
-            wp[2 * w + 1] = fmaf(ct, live ? f.y : 0.f, wp[2 * w + 1]);
-          } else {
-            wp[w] = fmaf(ct, live ? __uint_as_float(wd[w]) : 0.f, wp[w]);
+      for (int p = 0; p < NVB; ++p) sc_bits[p] = ld_u16_uniform((const uint16_t*)(scale_hv + ((v0 + r0) / kVBlock + p) * a.sc_v));
+      uint4 ck[NCH];
+      GDNR_COMPILER_FENCE();
+      {
+        // one uniform base, a 32-bit lane offset per 16-row block
+        const uint32_t rstep = 16u * (uint32_t)a.ck_v;
+#pragma unroll
+        for (int i = 0; i < NBLK; ++i) {
+          const uint32_t off = ck_lo + (uint32_t)i * rstep;
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh) ck[hh * NBLK + i] = *(const uint4*)(ck_rows + (off + 64u * hh));
+        }
+      }
+      GDNR_COMPILER_FENCE();
+      // the v rows land ahead of the checkpoint rows: copy them to LDS in
+      // token-major order (chunk c at byte 16 c) and free their registers
+      GDNR_WAIT_VMCNT(NCH);
+#pragma unroll
+      for (int i = 0; i < NV; ++i) *(u32x4_t*)(vbuf + 16 * (64 * i + lane)) = vch[i];
+      __hip_atomic_store(flags + 2 * a.gw + j_head, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+      await_coefficients();
+      // w = sum_t c_t v_t: per-lane partials over the lane's chunks (rows
+      // EPC rc + [0, EPC)), exchanged through LDS (this head's U~ area, unused
+      // by a replay) and summed per output row below
+      const float* part = (const float*)(lds + a.lds_u + j_head * LP * 192);  // [lane][EPC]
+      {
+        float wp[EPC];
+#pragma unroll
+        for (int e = 0; e < EPC; ++e) wp[e] = 0.f;
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+          const int t = (64 * i + lane) / CPT_V;
+          const bool live = t < n;
+          const float ct = live ? c_head[live ? t : 0] : 0.f;
+          const u32x4_t vc = *(const u32x4_t*)(vbuf + 16 * (64 * i + lane));
+          const uint32_t wd[4] = {vc[0], vc[1], vc[2], vc[3]};
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            if constexpr (ES == 2) {
+              const float2 f = Act::from_pair(wd[w]);
+              wp[2 * w] = fmaf(ct, live ? f.x : 0.f, wp[2 * w]);
+              wp[2 * w + 1] = fmaf(ct, live ? f.y : 0.f, wp[2 * w + 1]);
+            } else {
+              wp[w] = fmaf(ct, live ? __uint_as_float(wd[w]) : 0.f, wp[w]);
+            }
           }
         }
+#pragma unroll
+        for (int e = 0; e < EPC; e += 4)
+          *(float4*)(part + lane * EPC + e) = make_float4(wp[e], wp[e + 1], wp[e + 2], wp[e + 3]);
       }
+      // lane (l16, q4) holds, per block i, row 16 i + l16 at columns
+      // 64 hh + 16 q4 + [0, 16): partial dots, then a 4-lane butterfly over q4;
+      // one half (hh) of the columns at a time: 16 values of T0 in registers
+      float P[NBLK];
 #pragma unroll
-      for (int e = 0; e < EPC; e += 4)
-        *(float4*)(part + lane * EPC + e) = make_float4(wp[e], wp[e + 1], wp[e + 2], wp[e + 3]);
-    }
-    // lane (l16, q4) holds, per block i, row 16 i + l16 at columns
-    // 64 hh + 16 q4 + [0, 16): partial dots, then a 4-lane butterfly over q4;
-    // one half (hh) of the columns at a time: 16 values of T0 in registers
-    float P[NBLK];
+      for (int i = 0; i < NBLK; ++i) P[i] = 0.f;
 #pragma unroll
-    for (int i = 0; i < NBLK; ++i) P[i] = 0.f;
+      for (int hh = 0; hh < 2; ++hh) {
+        float Tv[16];
+        const float4* tp = (const float4*)(lds + a.lds_t + (j_head * K + 64 * hh + 16 * q4) * 4);
 #pragma unroll
-    for (int hh = 0; hh < 2; ++hh) {
-      float Tv[16];
-      const float4* tp = (const float4*)(lds + a.lds_t + (j_head * K + 64 * hh + 16 * q4) * 4);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float4 w = tp[i];
-        Tv[4 * i] = w.x;
-        Tv[4 * i + 1] = w.y;
-        Tv[4 * i + 2] = w.z;
-        Tv[4 * i + 3] = w.w;
-      }
-#pragma unroll
-      for (int i = 0; i < NBLK; ++i) {
-        const uint4 c = ck[hh * NBLK + i];
-        const uint32_t w4[4] = {c.x, c.y, c.z, c.w};
-        float p = P[i];
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          float f[4];
-          fp8x4_to_f32(w4[w], f);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) p = fmaf(f[e], Tv[4 * w + e], p);
+        for (int i = 0; i < 4; ++i) {
+          const float4 w = tp[i];
+          Tv[4 * i] = w.x;
+          Tv[4 * i + 1] = w.y;
+          Tv[4 * i + 2] = w.z;
+          Tv[4 * i + 3] = w.w;
         }
-        P[i] = p;
+#pragma unroll
+        for (int i = 0; i < NBLK; ++i) {
+          const uint4 c = ck[hh * NBLK + i];
+          const uint32_t w4[4] = {c.x, c.y, c.z, c.w};
+          float p = P[i];
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            float f[4];
+            fp8x4_to_f32(w4[w], f);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) p = fmaf(f[e], Tv[4 * w + e], p);
+          }
+          P[i] = p;
+        }
       }
-    }
-    // butterfly over q4 (lanes l16 + 16 q4): step 1 (xor 16) keeps the blocks
-    // with i % 2 == q4 % 2, step 2 (xor 32) those with (i / 2) % 2 == q4 / 2, so
-    // lane l ends with the totals of rows 64 m + l (NBLK >= 4), or lanes q4 and
-    // q4 ^ 2 both with row 16 (q4 % 2) + l16 (NBLK = 2)
-    const bool hi1 = (q4 & 1) != 0, hi2 = (q4 & 2) != 0;
-    float R2[NBLK / 2];
+      // butterfly over q4 (lanes l16 + 16 q4): step 1 (xor 16) keeps the blocks
+      // with i % 2 == q4 % 2, step 2 (xor 32) those with (i / 2) % 2 == q4 / 2, so
+      // lane l ends with the totals of rows 64 m + l (NBLK >= 4), or lanes q4 and
+      // q4 ^ 2 both with row 16 (q4 % 2) + l16 (NBLK = 2)
+      const bool hi1 = (q4 & 1) != 0, hi2 = (q4 & 2) != 0;
+      float R2[NBLK / 2];
 #pragma unroll
-    for (int m = 0; m < NBLK / 2; ++m) {
-      const float send = hi1 ? P[2 * m] : P[2 * m + 1];
-      const float keep = hi1 ? P[2 * m + 1] : P[2 * m];
-      R2[m] = keep + __shfl_xor(send, 16);
-    }
-    constexpr int NOUT = NBLK >= 4 ? NBLK / 4 : 1;
-#pragma unroll
-    for (int m = 0; m < NOUT; ++m) {
-      float tot;
-      int row;  // row within this head's block_v rows
-      if constexpr (NBLK >= 4) {
-        const float send = hi2 ? R2[2 * m] : R2[2 * m + 1];
-        const float keep = hi2 ? R2[2 * m + 1] : R2[2 * m];
-        tot = keep + __shfl_xor(send, 32);
-        row = 64 * m + lane;
-      } else {
-        tot = R2[0] + __shfl_xor(R2[0], 32);
-        row = 16 * (q4 & 1) + l16;
+      for (int m = 0; m < NBLK / 2; ++m) {
+        const float send = hi1 ? P[2 * m] : P[2 * m + 1];
+        const float keep = hi1 ? P[2 * m + 1] : P[2 * m];
+        R2[m] = keep + __shfl_xor(send, 16);
       }
-      // scale of the row's vblock: row >> 5 = 2 m + (lane >> 5) (NBLK >= 4), else 0
-      // (a bit-select: a plain select of the two entries is folded back into a
-      // lane-indexed load from a private array)
-      uint32_t sb = sc_bits[NBLK >= 4 ? 2 * m : 0];
-      if constexpr (NBLK >= 4) sb ^= (sb ^ sc_bits[2 * m + 1]) & (0u - (uint32_t)(lane >> 5));
-      const float sc = f16_bits_to_f32((uint16_t)sb);
-      float wrow = 0.f;
+      constexpr int NOUT = NBLK >= 4 ? NBLK / 4 : 1;
 #pragma unroll
-      for (int mm = 0; mm < 64 / CPT_V; ++mm) wrow += part[(row / EPC + CPT_V * mm) * EPC + row % EPC];
-      if (NBLK >= 4 || q4 < 2) Act::st(out_rows, row, fmaf(tot, sc, wrow) * a.out_scale);
+      for (int m = 0; m < NOUT; ++m) {
+        float tot;
+        int row;  // row within this head's block_v rows
+        if constexpr (NBLK >= 4) {
+          const float send = hi2 ? R2[2 * m] : R2[2 * m + 1];
+          const float keep = hi2 ? R2[2 * m + 1] : R2[2 * m];
+          tot = keep + __shfl_xor(send, 32);
+          row = 64 * m + lane;
+        } else {
+          tot = R2[0] + __shfl_xor(R2[0], 32);
+          row = 16 * (q4 & 1) + l16;
+        }
+        // scale of the row's vblock: row >> 5 = 2 m + (lane >> 5) (NBLK >= 4), else 0
+        // (a bit-select: a plain select of the two entries is folded back into a
+        // lane-indexed load from a private array)
+        uint32_t sb = sc_bits[NBLK >= 4 ? 2 * m : 0];
+        if constexpr (NBLK >= 4) sb ^= (sb ^ sc_bits[2 * m + 1]) & (0u - (uint32_t)(lane >> 5));
+        const float sc = f16_bits_to_f32((uint16_t)sb);
+        float wrow = 0.f;
+#pragma unroll
+        for (int mm = 0; mm < 64 / CPT_V; ++mm) wrow += part[(row / EPC + CPT_V * mm) * EPC + row % EPC];
+        if (NBLK >= 4 || q4 < 2) Act::st(out_rows, row, fmaf(tot, sc, wrow) * a.out_scale);
+      }
+      append_token();
+      return;
     }
-    append_token();
-    return;
+    // flush: no checkpoint rows in registers (section 7 reads them per vblock)
+    GDNR_WAIT_VMCNT(0);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) *(u32x4_t*)(vbuf + 16 * (64 * i + lane)) = vch[i];
+    __hip_atomic_store(flags + 2 * a.gw + j_head, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+    await_coefficients();
+    fp0 = 0, fp1 = NVB / 2, uoff = a.lds_u + j_head * LP * 192;
   }
 
-  // ---- 7. flush: MFMA rebuild of this wave's rows, emit, requantise in place
-  await_coefficients();
-  const XRows xr{a.lds_k, a.lds_knew, a.lds_q, n, pos};
-  // Per vblock p (32 rows = 16-row blocks 2p, 2p + 1) lane l owns row l % 16
-  // of a block; the contraction walks the columns in the order of ck, so every
-  // checkpoint operand comes straight from those registers and the
-  // requantised codes go back as the same two 16-byte words.
-  //   A.  P^T = [K; q] S_0^T          (tokens x rows; the q row gives S_0 q)
-  //       W^T = v - pre . P^T
-  //   B.  U^T = R W^T,  U~^T = post . U^T,  o = lam_all S_0 q + sum_t U~^T[t] (k_t . q)
-  //   C.  S_n^T = lam_all S_0^T + K^T U~^T, two passes over the vblock:
-  //       amax, then requantisation.
-  // W^T and U~^T tiles are parked in this wave's LDS area in the MFMA
-  // B-operand layout ([tile][lane], 16 bytes a lane).
-  {
-    const int ntbx = n < LP ? 1 : 2;  // token blocks including the q row at index n
-    const float* Rj = (const float*)(lds + a.lds_r) + j_head * LP * LP;
-    const float4* fac = (const float4*)(lds + a.lds_fac) + j_head * LP;
-    const float lam_all = ((const float*)(lds + a.lds_lam))[j_head];
-    uint4* ubuf = (uint4*)(lds + a.lds_u + j_head * LP * 192);  // U~^T: [block mm][lane]
-    float4* wbuf = (float4*)(ubuf + 2 * 64);                   // W^T:  [lane]
-    // codes of vblock p: cf[hh * 2 + mm] (the layout of ck), next vblock
-    // prefetched. The row pointer is laundered: the compiler must not fold
-    // these loads into the replay's ck registers (that would keep all of ck
-    // live through the rebuild).
-    uint4 cf[4], cn[4];
-    const uint8_t* ck_rows_f = ck_rows;
-    asm volatile("" : "+s"(ck_rows_f));
-    auto load_vb = [&](int p, uint4* d) {
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh)
-#pragma unroll
-        for (int mm = 0; mm < 2; ++mm)
-          d[hh * 2 + mm] = *(const uint4*)(ck_rows_f + ((32 * p + 16 * mm) * a.ck_v + 64 * hh + ck_lo));
-    };
-    load_vb(0, cf);
-#pragma unroll 1
-    for (int p = 0; p < NVB; ++p) {
-      if (p + 1 < NVB) load_vb(p + 1, cn);
-      const float sc = f16_bits_to_f32((uint16_t)ld_u16_uniform((const uint16_t*)(scale_hv + ((v0 + r0) / kVBlock + p) * a.sc_v)));
-#pragma unroll
-      for (int mm = 0; mm < 2; ++mm) {
-        const int blk = 2 * p + mm;
-        const int rl = 16 * blk + l16;  // row within this wave's rows
-        const uint4 c0 = cf[mm], c1 = cf[2 + mm];
-        const uint32_t cw[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
-        float o_part = 0.f;
-        // A: P^T blocks and W^T
-#pragma unroll 1
-        for (int tb = 0; tb < ntbx; ++tb) {
-          const int x = tb * 16 + l16;  // token row of X supplied by this lane
-          const bool zero_x = x > n;
-          f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-          if constexpr (BF16 || F16) {
-#pragma unroll
-            for (int m = 0; m < 4; ++m) {
-              // columns 64 (m / 2) + 16 q4 + 8 (m % 2) + [0, 8): words 2m, 2m + 1
-              uint4 av = *(const uint4*)(lds + xr.off<ROWB>(x, (64 * (m >> 1) + 16 * q4 + 8 * (m & 1)) * 2));
-              if (zero_x) av = make_uint4(0u, 0u, 0u, 0u);
-              float f[8];
-              fp8x4_to_f32(opaque(cw[2 * m]), f);
-              fp8x4_to_f32(opaque(cw[2 * m + 1]), f + 4);
-              if constexpr (BF16) {
-                // e4m3 values are exact in bf16
-                const uint4 bv = make_uint4(pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]), pack_bf16x2(f[4], f[5]),
-                                            pack_bf16x2(f[6], f[7]));
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, av),
-                                                              __builtin_bit_cast(bf16x8_t, bv), acc, 0, 0, 0);
-              } else {
-                const f16x8_t bv = {(_Float16)f[0], (_Float16)f[1], (_Float16)f[2], (_Float16)f[3],
-                                    (_Float16)f[4], (_Float16)f[5], (_Float16)f[6], (_Float16)f[7]};
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, av), bv, acc, 0, 0, 0);
-              }
-            }
-          } else {
-#pragma unroll
-            for (int kc = 0; kc < 8; ++kc) {
-              const int col = 64 * (kc >> 2) + 16 * q4 + 4 * (kc & 3);
-              float f[4];
-              fp8x4_to_f32(opaque(cw[kc]), f);
-#pragma unroll
-              for (int e = 0; e < 4; ++e) {
-                float av = *(const float*)(lds + xr.off<ROWB>(x, (col + e) * 4));
-                av = zero_x ? 0.f : av;
-                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av, f[e], acc, 0, 0, 0);
-              }
-            }
-          }
-          float wv[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int t = tb * 16 + 4 * q4 + e;
-            const float pv = acc[e] * sc;
-            if (t < n) {
-              wv[e] = Act::ld(vbuf, t * RPW + rl) - fac[t].x * pv;
-            } else {
-              wv[e] = 0.f;
-              if (t == n) o_part = fmaf(lam_all, pv, o_part);
-            }
-          }
-          // the block holding only the q row (tb == 1) is not a token block of W^T
-          if (tb == 0) wbuf[lane] = make_float4(wv[0], wv[1], wv[2], wv[3]);
-        }
-        // B: U^T = R W^T (fp32 MFMA, contraction index q4 <-> token 4 q4 + e)
-        {
-          f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-          const float4 wv = wbuf[lane];
-          const float* rrow = Rj + l16 * LP + 4 * q4;
-          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(rrow[0], wv.x, acc, 0, 0, 0);
-          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(rrow[1], wv.y, acc, 0, 0, 0);
-          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(rrow[2], wv.z, acc, 0, 0, 0);
-          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(rrow[3], wv.w, acc, 0, 0, 0);
-          float ut[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float4 f = fac[4 * q4 + e];
-            ut[e] = acc[e] * f.y;
-            o_part = fmaf(ut[e], f.z, o_part);
-          }
-          uint4 packed;
-          if constexpr (BF16) {
-            // hi/lo split: U~ = hi + lo to ~16 bits, both halves bf16 MFMA operands
-            const uint32_t h01 = pack_bf16x2(ut[0], ut[1]), h23 = pack_bf16x2(ut[2], ut[3]);
-            const uint32_t l01 =
-                pack_bf16x2(ut[0] - __uint_as_float(h01 << 16), ut[1] - __uint_as_float(h01 & 0xFFFF0000u));
-            const uint32_t l23 =
-                pack_bf16x2(ut[2] - __uint_as_float(h23 << 16), ut[3] - __uint_as_float(h23 & 0xFFFF0000u));
-            packed = make_uint4(h01, h23, l01, l23);
-          } else {
-            packed = make_uint4(__float_as_uint(ut[0]), __float_as_uint(ut[1]), __float_as_uint(ut[2]),
-                                __float_as_uint(ut[3]));
-          }
-          ubuf[mm * 64 + lane] = packed;
-        }
-        o_part += __shfl_xor(o_part, 16);
-        o_part += __shfl_xor(o_part, 32);
-        if (q4 == 0) Act::st(out_rows, rl, o_part * a.out_scale);
-      }
-      // C: S_n^T tiles sn[ct] of block mm (ct = 4 hh + w): D row 4 q4 + e of
-      // tile ct is column 64 hh + 16 q4 + 4 w + e, and row l16 of K^T tile ct
-      // (the A operand of lane l) holds that column ordering already. Two
-      // passes over the blocks: amax, then requantisation (the reference
-      // quantiser, ref:36-37,83-99: s = amax/448, 1 when amax is not > 0;
-      // codes = e4m3fn(clamp(x / s, +-448)) with the unrounded fp32 s).
-      float s32 = 1.f;
-#pragma unroll 1
-      for (int pass = 0; pass < 2; ++pass) {
-        uint32_t am = 0;
-#pragma unroll
-        for (int mm = 0; mm < 2; ++mm) {
-          const int blk = 2 * p + mm;
-          f32x4_t sn[8];
-#pragma unroll
-          for (int ct = 0; ct < 8; ++ct) {
-            const uint4 c = cf[(ct >> 2) * 2 + mm];
-            const uint32_t wd = (ct & 3) == 0 ? c.x : (ct & 3) == 1 ? c.y : (ct & 3) == 2 ? c.z : c.w;
-            float f[4];
-            fp8x4_to_f32(opaque(wd), f);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) sn[ct][e] = lam_all * (f[e] * sc);
-          }
-          const uint4 u = ubuf[mm * 64 + lane];
-          const uint8_t* kt_lane = lds + a.lds_kt + l16 * 16 * ES + 4 * q4 * ES;  // tokens 4 q4 + e
-#pragma unroll
-          for (int ct = 0; ct < 8; ++ct) {
-            const uint8_t* ktrow = kt_lane + ct * 256 * ES;
-            if constexpr (BF16) {
-              const bf16x4_t av = __builtin_bit_cast(bf16x4_t, *(const uint2*)ktrow);
-              sn[ct] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(av, __builtin_bit_cast(bf16x4_t, make_uint2(u.x, u.y)),
-                                                                 sn[ct], 0, 0, 0);
-              sn[ct] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(av, __builtin_bit_cast(bf16x4_t, make_uint2(u.z, u.w)),
-                                                                 sn[ct], 0, 0, 0);
-            } else {
-              const float uf[4] = {__uint_as_float(u.x), __uint_as_float(u.y), __uint_as_float(u.z),
-                                   __uint_as_float(u.w)};
-#pragma unroll
-              for (int e = 0; e < 4; ++e)
-                sn[ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(Act::ld(ktrow, e), uf[e], sn[ct], 0, 0, 0);
-            }
-          }
-          if (pass == 0) {
-#pragma unroll
-            for (int ct = 0; ct < 8; ++ct)
-#pragma unroll
-              for (int e = 0; e < 4; ++e) am = max(am, __float_as_uint(sn[ct][e]) & 0x7FFFFFFFu);
-          } else {
-            uint8_t* rp = ck_rows + ((16 * blk + l16) * a.ck_v + 16 * q4);
-#pragma unroll
-            for (int hh = 0; hh < 2; ++hh) {
-              uint32_t wd[4];
-#pragma unroll
-              for (int w = 0; w < 4; ++w) {
-                const f32x4_t& v = sn[4 * hh + w];
-                wd[w] = f32x4_to_fp8(clamp448(v[0] / s32), clamp448(v[1] / s32), clamp448(v[2] / s32),
-                                     clamp448(v[3] / s32));
-              }
-              *(uint4*)(rp + 64 * hh) = make_uint4(wd[0], wd[1], wd[2], wd[3]);
-            }
-          }
-        }
-        if (pass == 0) {
-          const float amax = __uint_as_float(wave_max_u32(am));
-          s32 = (amax > 0.0f) ? amax / 448.0f : 1.0f;
-        }
-      }
-      if (lane == 0)
-        *(uint16_t*)(scale_hv + ((v0 + r0) / kVBlock + p) * a.sc_v) = __builtin_bit_cast(uint16_t, (_Float16)s32);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) cf[i] = cn[i];
-    }
-  }
-  append_token();
+  // ---- 7. flush: MFMA rebuild of vblocks [fp0, fp1) of the head, out of line
+  flush_vblocks<Act, NCH>(ck_rows, scale_hv, out_rows, a.ck_v, a.sc_v, (v0 + r0) / kVBlock, a.out_scale, a.lds_k,
+                          a.lds_knew, a.lds_q, a.lds_r, a.lds_fac, a.lds_lam, a.lds_kt, (int32_t)(vbuf - lds), uoff,
+                          j_head, n, pos, fp0, fp1);
+  if (__builtin_amdgcn_readfirstlane((int)head_lead) == 0) append_token();
 }
 
 #if GDNR_ACT == 0

@@ -50,7 +50,34 @@ def _edge_state(device):
     x[1, 0, :32] *= 1e4                                # large magnitudes
     x[1, 1, :32] = torch.randint(-2000, 2000, (32, 128), generator=gen).float() / 256.0  # many ties
     x[1, 2, 64:96] = 1e-30 * torch.randn(32, 128, generator=gen)  # subnormal fp32 scale
+    x[1, 3, :32] = _near_midpoint_block(gen)           # quotients within a few ulp of fp8 midpoints
+    nan_block = torch.full((32, 128), 0.25)            # NaN amax: scale 1, NaN codes keep their sign
+    nan_block[4, 4], nan_block[5, 5], nan_block[0, 1] = float("nan"), -float("nan"), 1000.0
+    x[1, 3, 32:64] = nan_block
+    x[1, 3, 64:96] = 1e-25 * torch.randn(32, 128, generator=gen)  # scale below 2^-64: division path
+    x[0, 3, :32] = torch.arange(-2048, 2048).float().view(32, 128) * 2.0 ** -11  # fp8 subnormal ties
+    x[0, 3, 0, 0] = 448.0                              # (scale exactly 1)
     return x.to(device)
+
+
+def _near_midpoint_block(gen):
+    """A 32 x 128 block whose quotients x / s land within +-3 fp32 ulp of
+    e4m3fn rounding midpoints (and a few on fp8 values), s = amax / 448 with
+    a non-power-of-two amax: the quotients the fast quantiser path must round
+    exactly as the division does."""
+    amax = np.float32(1.2345)
+    s = np.float32(amax / np.float32(448.0))
+    exps = torch.randint(-6, 9, (32 * 128,), generator=gen).numpy()
+    mant = torch.randint(0, 8, (32 * 128,), generator=gen).numpy()
+    mid = (1.0 + (2 * mant + 1) / 16.0) * np.exp2(exps.astype(np.float64))  # midpoints of the fp8 grid
+    mid = np.minimum(mid, 440.0)
+    ulps = torch.randint(-3, 4, (32 * 128,), generator=gen).numpy()
+    q = mid * (1.0 + ulps * 2.0 ** -23)
+    sign = np.where(torch.rand(32 * 128, generator=gen).numpy() < 0.5, -1.0, 1.0)
+    x = np.float32(sign * q * np.float64(s))
+    x = np.clip(x, -amax, amax)
+    x[0] = amax
+    return torch.from_numpy(x.reshape(32, 128).astype(np.float32))
 
 
 @pytest.mark.parametrize("kind", ["random", "edge"])
