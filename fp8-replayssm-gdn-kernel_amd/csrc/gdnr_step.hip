@@ -246,6 +246,26 @@ __device__ __attribute__((noinline)) void flush_vblocks(
         const uint4 c0 = cf[mm], c1 = cf[2 + mm];
         const uint32_t cw[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
         float o_part = 0.f;
+        // the codes of the block as 16-bit MFMA B operands, once for every
+        // token block (e4m3 values are exact in bf16 and f16): k-step m holds
+        // columns 64 (m / 2) + 16 q4 + 8 (m % 2) + [0, 8), words 2m, 2m + 1
+        uint4 bvs[4];
+        if constexpr (BF16 || F16) {
+#pragma unroll
+          for (int m = 0; m < 4; ++m) {
+            float fv[8];
+            fp8x4_to_f32(cw[2 * m], fv);
+            fp8x4_to_f32(cw[2 * m + 1], fv + 4);
+            if constexpr (BF16) {
+              bvs[m] = make_uint4(pack_bf16x2(fv[0], fv[1]), pack_bf16x2(fv[2], fv[3]), pack_bf16x2(fv[4], fv[5]),
+                                  pack_bf16x2(fv[6], fv[7]));
+            } else {
+              const f16x8_t h = {(_Float16)fv[0], (_Float16)fv[1], (_Float16)fv[2], (_Float16)fv[3],
+                                 (_Float16)fv[4], (_Float16)fv[5], (_Float16)fv[6], (_Float16)fv[7]};
+              bvs[m] = __builtin_bit_cast(uint4, h);
+            }
+          }
+        }
         // A: P^T blocks and W^T
 #pragma unroll 1
         for (int tb = 0; tb < ntbx; ++tb) {
@@ -255,23 +275,14 @@ __device__ __attribute__((noinline)) void flush_vblocks(
           if constexpr (BF16 || F16) {
 #pragma unroll
             for (int m = 0; m < 4; ++m) {
-              // columns 64 (m / 2) + 16 q4 + 8 (m % 2) + [0, 8): words 2m, 2m + 1
               uint4 av = *(const uint4*)(lds + xr.off<ROWB>(x, (64 * (m >> 1) + 16 * q4 + 8 * (m & 1)) * 2));
               if (zero_x) av = make_uint4(0u, 0u, 0u, 0u);
-              float f[8];
-              fp8x4_to_f32(opaque(cw[2 * m]), f);
-              fp8x4_to_f32(opaque(cw[2 * m + 1]), f + 4);
-              if constexpr (BF16) {
-                // e4m3 values are exact in bf16
-                const uint4 bv = make_uint4(pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]), pack_bf16x2(f[4], f[5]),
-                                            pack_bf16x2(f[6], f[7]));
+              if constexpr (BF16)
                 acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, av),
-                                                              __builtin_bit_cast(bf16x8_t, bv), acc, 0, 0, 0);
-              } else {
-                const f16x8_t bv = {(_Float16)f[0], (_Float16)f[1], (_Float16)f[2], (_Float16)f[3],
-                                    (_Float16)f[4], (_Float16)f[5], (_Float16)f[6], (_Float16)f[7]};
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, av), bv, acc, 0, 0, 0);
-              }
+                                                              __builtin_bit_cast(bf16x8_t, bvs[m]), acc, 0, 0, 0);
+              else
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, av),
+                                                             __builtin_bit_cast(f16x8_t, bvs[m]), acc, 0, 0, 0);
             }
           } else {
 #pragma unroll
@@ -352,6 +363,24 @@ __device__ __attribute__((noinline)) void flush_vblocks(
       // is finite).
       f32x4_t sn[2][8];
       uint32_t am = 0;
+      // bf16: lam_all scale S_0^T enters through the MFMA as (ls I) S_0^T with
+      // ls = lam_all * scale split into bf16 hi + lo (relative error 2^-18);
+      // lane (l16, q4) supplies row l16, columns 4 q4 + e of the identity
+      bf16x4_t a2hi, a2lo;
+      if constexpr (BF16) {
+        const float ls = lam_all * sc;
+        const uint32_t hb = f32_to_bf16(ls);
+        const uint32_t lb = f32_to_bf16(ls - __uint_as_float(hb << 16));
+        short h4[4], l4[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const bool diag = l16 == 4 * q4 + e;
+          h4[e] = (short)(diag ? hb : 0u);
+          l4[e] = (short)(diag ? lb : 0u);
+        }
+        a2hi = bf16x4_t{h4[0], h4[1], h4[2], h4[3]};
+        a2lo = bf16x4_t{l4[0], l4[1], l4[2], l4[3]};
+      }
 #pragma unroll
       for (int mm = 0; mm < 2; ++mm) {
 #pragma unroll
@@ -360,8 +389,15 @@ __device__ __attribute__((noinline)) void flush_vblocks(
           const uint32_t wd = (ct & 3) == 0 ? c.x : (ct & 3) == 1 ? c.y : (ct & 3) == 2 ? c.z : c.w;
           float f[4];
           fp8x4_to_f32(wd, f);
+          if constexpr (BF16) {
+            const bf16x4_t b2 = __builtin_bit_cast(bf16x4_t, make_uint2(pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3])));
+            const f32x4_t z = {0.f, 0.f, 0.f, 0.f};
+            sn[mm][ct] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a2hi, b2, z, 0, 0, 0);
+            sn[mm][ct] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a2lo, b2, sn[mm][ct], 0, 0, 0);
+          } else {
 #pragma unroll
-          for (int e = 0; e < 4; ++e) sn[mm][ct][e] = lam_all * (f[e] * sc);
+            for (int e = 0; e < 4; ++e) sn[mm][ct][e] = lam_all * (f[e] * sc);
+          }
         }
         if (mm == 1 && p + 1 < fp1) load_vb(p + 1, cf);  // the codes of vblock p are consumed
         const uint4 u = ubuf[mm * 64 + lane];
@@ -383,10 +419,13 @@ __device__ __attribute__((noinline)) void flush_vblocks(
               sn[mm][ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(Act::ld(ktrow, e), uf[e], sn[mm][ct], 0, 0, 0);
           }
         }
+        // |x| max on the bit patterns (NaN propagates like torch.amax); pairs form v_max3
 #pragma unroll
         for (int ct = 0; ct < 8; ++ct)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) am = max(am, __float_as_uint(sn[mm][ct][e]) & 0x7FFFFFFFu);
+          for (int e = 0; e < 4; e += 2)
+            am = max(am, max(__float_as_uint(sn[mm][ct][e]) & 0x7FFFFFFFu,
+                             __float_as_uint(sn[mm][ct][e + 1]) & 0x7FFFFFFFu));
       }
       const uint32_t amb = wave_max_u32(am);
       const float amax = __uint_as_float(amb);
