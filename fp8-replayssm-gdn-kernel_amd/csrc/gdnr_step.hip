@@ -6,19 +6,23 @@
 // head h, z = sequence b (no integer division on the way to the first load).
 // Workgroup = gw value heads sharing key head h, block_v V-rows of each, and
 // two waves per head:
-//   lead j (wave j): loads the k ring (all L slots; slots beyond the fill are
-//     read and ignored), q and the gates, then the v rows of head j; prepares
-//     the new token (fused), forms the Gram matrix and the coefficient chain
-//     of head j, folds the v rows into w = sum_t c_t v_t, and publishes
-//     through an LDS flag. It loads no checkpoint row: a wave whose loads
-//     back up in the memory pipeline cannot issue anything else, and the
-//     checkpoint stream would stall the chain.
-//   streamer j (wave gw + j): owns the block_v rows of head j -- vblock
-//     scales and NCH = block_v / 8 checkpoint loads of 16 bytes a lane in the
-//     MFMA operand layout (lane (l16, q4) of 16-row block i holds row l16,
-//     bytes [16 q4, +16) and [64 + 16 q4, +16)), which serves both the replay
-//     matvec and the flush rebuild. It requests them at once, waits for the
-//     coefficients, then emits its rows and appends the new token.
+//   lead j (wave j): loads its share of the k ring (all L slots split over
+//     the leads by direct-to-LDS DMA; slots beyond the fill are read and
+//     ignored), q and the gates; prepares the new token (fused), forms the
+//     Gram matrix and the coefficient chain of head j (c_t and T0 of a
+//     replay, the rebuild factors of a flush) and publishes them through an
+//     LDS flag. It loads no checkpoint row: a wave whose loads back up in the
+//     memory pipeline cannot issue anything else, and the checkpoint stream
+//     would stall the chain.
+//   streamer j (wave gw + j): waits until the whole k ring has landed, then
+//     requests the v rows of head j and its block_v checkpoint rows -- vblock
+//     scales and NCH = block_v / 8 loads of 16 bytes a lane in the MFMA
+//     operand layout (lane (l16, q4) of 16-row block i holds row l16, bytes
+//     [16 q4, +16) and [64 + 16 q4, +16)), which serves both the replay
+//     matvec and the flush rebuild. It stages the v rows in LDS, waits for the
+//     coefficients, folds w = sum_t c_t v_t, emits its rows and appends the
+//     new token. A flush splits the head's vblocks between the streamer and
+//     the lead once both have published.
 //
 // Replay, the adjoint of the reference's reverse chain
 // (prototype/gdn_replayssm_fp8_kernel.py:121-173), in Gram form:
@@ -533,13 +537,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
   // (the 16-byte chunks of all L slots split over the gw leads by
   // direct-to-LDS DMA; slots beyond the fill are read and ignored), q (lead
   // 0; fused: q and k of the new token in every lead), the gates of its head
-  // -- before the workgroup barrier B0, after which the streamers request the
-  // checkpoint: the ring requests of the grid reach memory first. It raises
-  // flags[gw + j] when they have landed and waits for the other leads'
-  // shares. The v rows of its head (the filled slots, once the metadata is
-  // in) follow into VGPRs: no LDS DMA may be pending while the lead touches
-  // LDS, or every LDS access would wait for it. The lead folds them into
-  // w = sum_t c_t v_t (replay) or stages them in LDS (flush).
+  // -- right after the workgroup barrier B0; the streamers request nothing until
+  // every share has landed, so the ring requests of the grid reach memory
+  // ahead of the checkpoint stream. It raises flags[gw + j] when its share
+  // has landed and waits for the other leads' shares.
   uint8_t* vbuf = lds + a.lds_v + j_head * LP * RPW * ES;
   float* c_head = (float*)(lds + a.lds_c) + j_head * RPW;  // c_t of head j (replay)
   // checkpoint rows (replay): ck[hh * NBLK + i] = row 16 i + l16, bytes
