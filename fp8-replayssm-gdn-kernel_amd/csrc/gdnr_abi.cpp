@@ -225,7 +225,8 @@ int fit_lds(gdnr::ReplayArgs* a, int es, bool stage_k, bool stage_v) {
 
 // LDS plan of the step kernel (gdnr_step.hip, L <= kStepRing) for the
 // current gw / block_v: q | new k | k ring | flags | c | T0 | slot Gram per head |
-// v rows | flush: R | factors | K^T tiles | lam_all | U~/W tiles (two waves a head).
+// v rows | flush: R | factors | K^T tiles | lam_all | per-head scratch (w partials of a
+// replay, decays and M of the flush factors).
 int32_t layout_step(gdnr::ReplayArgs* a, int es) {
   const int64_t K = gdnr::kKeyDim, LP = gdnr::kStepRing;
   a->rpw = a->block_v;  // one streamer wave per head owns the head's block_v rows
@@ -238,7 +239,8 @@ int32_t layout_step(gdnr::ReplayArgs* a, int es) {
   region(&a->lds_q, K * es);
   region(&a->lds_knew, K * es);
   region(&a->lds_k, (int64_t)a->L * K * es);
-  region(&a->lds_flag, (int64_t)a->gw * 20);  // 3 flags + new (gamma, beta) per head
+  // per head: 3 flags, the new (gamma, beta), the flush amax exchange words
+  region(&a->lds_flag, (int64_t)a->gw * 4 * (5 + 2 * gdnr::kMaxVBlocks));
   region(&a->lds_c, (int64_t)a->gw * a->block_v * 4);  // c_t per head (replay)
   region(&a->lds_t, (int64_t)a->gw * K * 4);
   region(&a->lds_g, (int64_t)a->gw * (LP + 2) * 20 * 4);  // [slots, q, new k]^2, row stride 20
@@ -247,7 +249,7 @@ int32_t layout_step(gdnr::ReplayArgs* a, int es) {
   region(&a->lds_fac, (int64_t)a->gw * LP * 16);
   region(&a->lds_kt, K * LP * es);
   region(&a->lds_lam, (int64_t)a->gw * 4);
-  region(&a->lds_u, (int64_t)2 * a->gw * LP * 192);  // U~/W scratch per flushing wave
+  region(&a->lds_u, (int64_t)a->gw * LP * 192);  // per-head scratch
   a->lds_bytes = (int32_t)off;
   return a->lds_bytes;
 }

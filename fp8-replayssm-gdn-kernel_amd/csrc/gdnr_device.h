@@ -149,6 +149,18 @@ __device__ __forceinline__ void fp8x4_to_f32(uint32_t w, float* f) {
   f[2] = hi[0];
   f[3] = hi[1];
 }
+// 4 e4m3 codes -> 4 bf16 values, packed in pairs (codes 0, 1 | codes 2, 3):
+// every e4m3 value, subnormals included, is exact in bf16; scale 1.0 makes
+// the scaled convert a plain one.
+__device__ __forceinline__ uint2 fp8x4_to_bf16x4(uint32_t w) {
+  return make_uint2(__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, false)),
+                    __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, true)));
+}
+// the same for f16 (every e4m3 value is exact in f16)
+__device__ __forceinline__ uint2 fp8x4_to_f16x4(uint32_t w) {
+  return make_uint2(__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, false)),
+                    __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, true)));
+}
 // 4 floats -> 4 packed codes, round-to-nearest-even (inputs already clamped).
 __device__ __forceinline__ uint32_t f32x4_to_fp8(float a, float b, float c, float d) {
   int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
@@ -179,12 +191,14 @@ __device__ __forceinline__ uint32_t f32x4_to_fp8_ref(float a, float b, float c, 
 // 1 ulp of x / s, no underflow or overflow). Callers use it only when the
 // block's amax is finite and s >= 2^-64, so |x / s| <= 448 (1 + 2^-23) and
 // every quotient the fp8 code depends on (|x / s| >= 2^-10) is a normal
-// number; the corrections turn -0 into +0, so the sign is restored.
+// number. The residual is formed negated, d = s q - x: a zero quotient then
+// keeps the sign of x (q - d r with d = +0 is q itself), as IEEE division
+// keeps it, with no separate sign fix.
 __device__ __forceinline__ float quotient_rn(float x, float s, float r) {
   float q = x * r;
-  q = fmaf(fmaf(-q, s, x), r, q);
-  q = fmaf(fmaf(-q, s, x), r, q);
-  return __builtin_copysignf(q, x);
+  q = fmaf(-fmaf(q, s, -x), r, q);
+  q = fmaf(-fmaf(q, s, -x), r, q);
+  return q;
 }
 // Whether a block with this amax (bits of |x| max) and scale takes quotient_rn:
 // amax finite and s >= 2^-64.

@@ -13,6 +13,7 @@ enum DType : int32_t {
 
 constexpr int kKeyDim = 128;      // K: the only head_k_dim built (Qwen3.5 / Qwen3-Next GDN)
 constexpr int kVBlock = 32;       // V-rows per checkpoint scale
+constexpr int kMaxVBlocks = 4;    // vblocks per step-kernel V-tile (block_v <= 128)
 constexpr int kMaxRing = 64;      // ring capacity bound (one VGPR lane per token)
 constexpr int kMaxWavesPerWG = 4; // value heads per workgroup (one wave each)
 

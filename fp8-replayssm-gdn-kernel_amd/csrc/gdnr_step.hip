@@ -160,8 +160,9 @@ struct FlushArgs {
   uint32_t ck_v, sc_v;  // row / vblock byte strides
   int32_t sc_row0;      // first vblock of the rows
   float out_scale;
-  int32_t lds_k, lds_knew, lds_q, lds_r, lds_fac, lds_lam, lds_kt, vbuf, uoff;
-  int32_t j_head, n, pos, fp0, fp1;  // head, ring fill, new slot, vblocks [fp0, fp1)
+  int32_t lds_k, lds_knew, lds_q, lds_r, lds_fac, lds_lam, lds_kt, vbuf;
+  int32_t lds_xam;  // amax exchange of the head: [block][vblock] words
+  int32_t j_head, n, pos, mm, nvb;  // head, ring fill, new slot, 16-row block of each vblock, vblocks
 };
 
 __device__ __forceinline__ int32_t uni(int32_t x) { return __builtin_amdgcn_readfirstlane(x); }
@@ -176,14 +177,19 @@ __device__ __forceinline__ uint8_t* uni(uint8_t* p) {
   return (uint8_t*)(((uint64_t)(uint32_t)uni((int32_t)(v >> 32)) << 32) | (uint32_t)uni((int32_t)v));
 }
 
+// The two waves of a head rebuild one 16-row block each (mm = 0 streamer,
+// mm = 1 lead) of every vblock of the head, and exchange the block amax per
+// vblock through LDS: a word per (block, vblock), cleared at kernel start,
+// written once as amax bits | 2^31 (amax bits are below 2^31).
 template <class Act, int NCH>
 __device__ __attribute__((noinline)) void flush_vblocks(
     uint8_t* f_ck_rows, uint8_t* f_scale_hv, uint8_t* f_out_rows, uint32_t f_ck_v, uint32_t f_sc_v, int32_t f_sc_row0,
     float f_out_scale, int32_t f_lds_k, int32_t f_lds_knew, int32_t f_lds_q, int32_t f_lds_r, int32_t f_lds_fac,
-    int32_t f_lds_lam, int32_t f_lds_kt, int32_t f_vbuf, int32_t f_uoff, int32_t f_j_head, int32_t f_n, int32_t f_pos,
-    int32_t f_fp0, int32_t f_fp1) {
-  FlushArgs f{f_ck_rows, f_scale_hv, f_out_rows, f_ck_v, f_sc_v, f_sc_row0, f_out_scale, f_lds_k, f_lds_knew, f_lds_q,
-              f_lds_r, f_lds_fac, f_lds_lam, f_lds_kt, f_vbuf, f_uoff, f_j_head, f_n, f_pos, f_fp0, f_fp1};
+    int32_t f_lds_lam, int32_t f_lds_kt, int32_t f_vbuf, int32_t f_lds_xam, int32_t f_j_head, int32_t f_n,
+    int32_t f_pos, int32_t f_mm, int32_t f_nvb) {
+  FlushArgs f{f_ck_rows, f_scale_hv, f_out_rows, f_ck_v,  f_sc_v,    f_sc_row0, f_out_scale, f_lds_k,
+              f_lds_knew, f_lds_q,   f_lds_r,  f_lds_fac, f_lds_lam, f_lds_kt,  f_vbuf,      f_lds_xam,
+              f_j_head,   f_n,       f_pos,    f_mm,      f_nvb};
   constexpr int ES = Act::kBytes;
   constexpr int ROWB = K * ES;
   constexpr int RPW = 8 * NCH;
@@ -191,11 +197,11 @@ __device__ __attribute__((noinline)) void flush_vblocks(
   constexpr bool F16 = std::is_same<Act, ActF16>::value;
   const int lane = threadIdx.x & 63;
   const int q4 = lane >> 4, l16 = lane & 15;
-  const int j_head = uni(f.j_head), n = uni(f.n), pos = uni(f.pos), fp0 = uni(f.fp0), fp1 = uni(f.fp1);
-  const int uoff = uni(f.uoff);
+  const int j_head = uni(f.j_head), n = uni(f.n), pos = uni(f.pos), mm = uni(f.mm), nvb = uni(f.nvb);
   const uint32_t ck_v = (uint32_t)uni((int32_t)f.ck_v), sc_v = (uint32_t)uni((int32_t)f.sc_v);
   f.sc_row0 = uni(f.sc_row0), f.lds_k = uni(f.lds_k), f.lds_knew = uni(f.lds_knew), f.lds_q = uni(f.lds_q);
   f.lds_r = uni(f.lds_r), f.lds_fac = uni(f.lds_fac), f.lds_lam = uni(f.lds_lam), f.lds_kt = uni(f.lds_kt);
+  f.lds_xam = uni(f.lds_xam);
   f.out_scale = __builtin_bit_cast(float, uni(__builtin_bit_cast(int32_t, f.out_scale)));
   uint8_t* ck_rows = uni(f.ck_rows);
   uint8_t* scale_hv = uni(f.scale_hv);
@@ -203,174 +209,152 @@ __device__ __attribute__((noinline)) void flush_vblocks(
   const uint8_t* vbuf = lds + uni(f.vbuf);
   const uint32_t ck_lo = (uint32_t)l16 * ck_v + 16 * q4;
   const XRows xr{f.lds_k, f.lds_knew, f.lds_q, n, pos};
-  // Per vblock p (32 rows = 16-row blocks 2p, 2p + 1) lane l owns row l % 16
-  // of a block; the contraction walks the columns in the order of ck, so every
+  int* xam_mine = (int*)(lds + f.lds_xam) + mm * kMaxVBlocks;
+  int* xam_other = (int*)(lds + f.lds_xam) + (1 - mm) * kMaxVBlocks;
+  // Per vblock p, block mm (rows 32 p + 16 mm + [0, 16)): lane l owns row
+  // l % 16; the contraction walks the columns in the order of ck, so every
   // checkpoint operand comes straight from those registers and the
   // requantised codes go back as the same two 16-byte words.
   //   A.  P^T = [K; q] S_0^T          (tokens x rows; the q row gives S_0 q)
   //       W^T = v - pre . P^T
   //   B.  U^T = R W^T,  U~^T = post . U^T,  o = lam_all S_0 q + sum_t U~^T[t] (k_t . q)
-  //   C.  S_n^T = lam_all S_0^T + K^T U~^T, two passes over the vblock:
-  //       amax, then requantisation.
-  // W^T and U~^T tiles are parked in this wave's LDS area in the MFMA
-  // B-operand layout ([tile][lane], 16 bytes a lane).
+  //   C.  S_n^T = lam_all S_0^T + K^T U~^T
+  // The accumulator of each step is, lane for lane, the B operand of the next
+  // (lane (l16, q4) holds tokens 4 q4 + e of row l16), so W^T and U~^T stay
+  // in registers. Then the vblock amax (this block's and the other wave's)
+  // and the requantisation of this block.
   {
-    const int ntbx = n < LP ? 1 : 2;  // token blocks including the q row at index n
     const float* Rj = (const float*)(lds + f.lds_r) + j_head * LP * LP;
     const float4* fac = (const float4*)(lds + f.lds_fac) + j_head * LP;
     const float lam_all = ((const float*)(lds + f.lds_lam))[j_head];
-    uint4* ubuf = (uint4*)(lds + uoff);  // U~^T: [block mm][lane]
-    float4* wbuf = (float4*)(ubuf + 2 * 64);                   // W^T:  [lane]
-    // codes of vblock p: cf[hh * 2 + mm] (the layout of ck); the next
+    // codes of this block of vblock p: cf[hh] (the layout of ck); the next
     // vblock's are requested into the same registers as soon as the rebuild
     // has consumed them. The row pointer is laundered: the compiler must not
     // fold these loads into the replay's ck registers (that would keep all of
     // ck live through the rebuild).
-    uint4 cf[4];
+    uint4 cf[2];
     const uint8_t* ck_rows_f = ck_rows;
     asm volatile("" : "+s"(ck_rows_f));
-    auto load_vb = [&](int p, uint4* d) {
+    auto load_blk = [&](int p) {
 #pragma unroll
-      for (int hh = 0; hh < 2; ++hh)
-#pragma unroll
-        for (int mm = 0; mm < 2; ++mm)
-        {
-          const u32x4_t w = *gptr<const u32x4_t>(ck_rows_f + ((32 * p + 16 * mm) * ck_v + 64 * hh + ck_lo));
-          d[hh * 2 + mm] = make_uint4(w[0], w[1], w[2], w[3]);
-        }
+      for (int hh = 0; hh < 2; ++hh) {
+        const u32x4_t w = *gptr<const u32x4_t>(ck_rows_f + ((32 * p + 16 * mm) * ck_v + 64 * hh + ck_lo));
+        cf[hh] = make_uint4(w[0], w[1], w[2], w[3]);
+      }
     };
-    if (fp0 < fp1) load_vb(fp0, cf);
+    load_blk(0);
 #pragma unroll 1
-    for (int p = fp0; p < fp1; ++p) {
+    for (int p = 0; p < nvb; ++p) {
       const float sc = f16_bits_to_f32((uint16_t)ld_u16_uniform((const uint16_t*)(scale_hv + (f.sc_row0 + p) * sc_v)));
+      const int rl = 32 * p + 16 * mm + l16;  // row within the head's rows
+      const uint32_t cw[8] = {cf[0].x, cf[0].y, cf[0].z, cf[0].w, cf[1].x, cf[1].y, cf[1].z, cf[1].w};
+      float o_part = 0.f;
+      // the codes of the block as 16-bit MFMA B operands, once for A and C
+      // (e4m3 values are exact in bf16 and f16): k-step m holds columns
+      // 64 (m / 2) + 16 q4 + 8 (m % 2) + [0, 8), words 2m, 2m + 1
+      uint4 bvs[4];
+      if constexpr (BF16 || F16) {
 #pragma unroll
-      for (int mm = 0; mm < 2; ++mm) {
-        const int blk = 2 * p + mm;
-        const int rl = 16 * blk + l16;  // row within this wave's rows
-        const uint4 c0 = cf[mm], c1 = cf[2 + mm];
-        const uint32_t cw[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
-        float o_part = 0.f;
-        // the codes of the block as 16-bit MFMA B operands, once for every
-        // token block (e4m3 values are exact in bf16 and f16): k-step m holds
-        // columns 64 (m / 2) + 16 q4 + 8 (m % 2) + [0, 8), words 2m, 2m + 1
-        uint4 bvs[4];
+        for (int m = 0; m < 4; ++m) {
+          const uint2 b0 = BF16 ? fp8x4_to_bf16x4(cw[2 * m]) : fp8x4_to_f16x4(cw[2 * m]);
+          const uint2 b1 = BF16 ? fp8x4_to_bf16x4(cw[2 * m + 1]) : fp8x4_to_f16x4(cw[2 * m + 1]);
+          bvs[m] = make_uint4(b0.x, b0.y, b1.x, b1.y);
+        }
+        if (p + 1 < nvb) load_blk(p + 1);  // the codes of vblock p are consumed
+      }
+      // A: P^T of the token block (rows x >= n read the q row: row n is S_0 q,
+      // the rows past it are never used) and W^T
+      auto x_times_s0 = [&](auto row_off) {  // row_off(by): LDS offset of this lane's X row at byte by
+        f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
         if constexpr (BF16 || F16) {
 #pragma unroll
           for (int m = 0; m < 4; ++m) {
-            float fv[8];
-            fp8x4_to_f32(cw[2 * m], fv);
-            fp8x4_to_f32(cw[2 * m + 1], fv + 4);
-            if constexpr (BF16) {
-              bvs[m] = make_uint4(pack_bf16x2(fv[0], fv[1]), pack_bf16x2(fv[2], fv[3]), pack_bf16x2(fv[4], fv[5]),
-                                  pack_bf16x2(fv[6], fv[7]));
-            } else {
-              const f16x8_t h = {(_Float16)fv[0], (_Float16)fv[1], (_Float16)fv[2], (_Float16)fv[3],
-                                 (_Float16)fv[4], (_Float16)fv[5], (_Float16)fv[6], (_Float16)fv[7]};
-              bvs[m] = __builtin_bit_cast(uint4, h);
-            }
+            const uint4 av = *(const uint4*)(lds + row_off((64 * (m >> 1) + 16 * q4 + 8 * (m & 1)) * 2));
+            if constexpr (BF16)
+              acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, av),
+                                                            __builtin_bit_cast(bf16x8_t, bvs[m]), acc, 0, 0, 0);
+            else
+              acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, av),
+                                                           __builtin_bit_cast(f16x8_t, bvs[m]), acc, 0, 0, 0);
+          }
+        } else {
+#pragma unroll
+          for (int kc = 0; kc < 8; ++kc) {
+            const int col = 64 * (kc >> 2) + 16 * q4 + 4 * (kc & 3);
+            float fa[4];
+            fp8x4_to_f32(opaque(cw[kc]), fa);
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              acc = __builtin_amdgcn_mfma_f32_16x16x4f32(*(const float*)(lds + row_off((col + e) * 4)), fa[e], acc, 0,
+                                                         0, 0);
           }
         }
-        // A: P^T blocks and W^T
-#pragma unroll 1
-        for (int tb = 0; tb < ntbx; ++tb) {
-          const int x = tb * 16 + l16;  // token row of X supplied by this lane
-          const bool zero_x = x > n;
-          f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-          if constexpr (BF16 || F16) {
+        return acc;
+      };
+      float wv[4];
+      {
+        const f32x4_t acc = x_times_s0([&](int by) { return xr.off<ROWB>(l16, by); });
+        // branch-free: every lane reads a valid token's v and factors
 #pragma unroll
-            for (int m = 0; m < 4; ++m) {
-              uint4 av = *(const uint4*)(lds + xr.off<ROWB>(x, (64 * (m >> 1) + 16 * q4 + 8 * (m & 1)) * 2));
-              if (zero_x) av = make_uint4(0u, 0u, 0u, 0u);
-              if constexpr (BF16)
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, av),
-                                                              __builtin_bit_cast(bf16x8_t, bvs[m]), acc, 0, 0, 0);
-              else
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, av),
-                                                             __builtin_bit_cast(f16x8_t, bvs[m]), acc, 0, 0, 0);
-            }
-          } else {
-#pragma unroll
-            for (int kc = 0; kc < 8; ++kc) {
-              const int col = 64 * (kc >> 2) + 16 * q4 + 4 * (kc & 3);
-              float f[4];
-              fp8x4_to_f32(opaque(cw[kc]), f);
-#pragma unroll
-              for (int e = 0; e < 4; ++e) {
-                float av = *(const float*)(lds + xr.off<ROWB>(x, (col + e) * 4));
-                av = zero_x ? 0.f : av;
-                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av, f[e], acc, 0, 0, 0);
-              }
-            }
-          }
-          float wv[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int t = tb * 16 + 4 * q4 + e;
-            const float pv = acc[e] * sc;
-            if (t < n) {
-              wv[e] = Act::ld(vbuf, t * RPW + rl) - fac[t].x * pv;
-            } else {
-              wv[e] = 0.f;
-              if (t == n) o_part = fmaf(lam_all, pv, o_part);
-            }
-          }
-          // the block holding only the q row (tb == 1) is not a token block of W^T
-          if (tb == 0) wbuf[lane] = make_float4(wv[0], wv[1], wv[2], wv[3]);
-        }
-        // B: U^T = R W^T (fp32 MFMA, contraction index q4 <-> token 4 q4 + e)
-        {
-          f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-          const float4 wv = wbuf[lane];
-          const float* rrow = Rj + l16 * LP + 4 * q4;
-          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(rrow[0], wv.x, acc, 0, 0, 0);
-          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(rrow[1], wv.y, acc, 0, 0, 0);
-          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(rrow[2], wv.z, acc, 0, 0, 0);
-          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(rrow[3], wv.w, acc, 0, 0, 0);
-          float ut[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float4 f = fac[4 * q4 + e];
-            ut[e] = acc[e] * f.y;
-            o_part = fmaf(ut[e], f.z, o_part);
-          }
-          uint4 packed;
-          if constexpr (BF16) {
-            // hi/lo split: U~ = hi + lo to ~16 bits, both halves bf16 MFMA operands
-            const uint32_t h01 = pack_bf16x2(ut[0], ut[1]), h23 = pack_bf16x2(ut[2], ut[3]);
-            const uint32_t l01 =
-                pack_bf16x2(ut[0] - __uint_as_float(h01 << 16), ut[1] - __uint_as_float(h01 & 0xFFFF0000u));
-            const uint32_t l23 =
-                pack_bf16x2(ut[2] - __uint_as_float(h23 << 16), ut[3] - __uint_as_float(h23 & 0xFFFF0000u));
-            packed = make_uint4(h01, h23, l01, l23);
-          } else {
-            packed = make_uint4(__float_as_uint(ut[0]), __float_as_uint(ut[1]), __float_as_uint(ut[2]),
-                                __float_as_uint(ut[3]));
-          }
-          ubuf[mm * 64 + lane] = packed;
-        }
-        o_part += __shfl_xor(o_part, 16);
-        o_part += __shfl_xor(o_part, 32);
-        if (q4 == 0) {
-          const float o = o_part * f.out_scale;
-          if constexpr (ES == 4) *gptr<float>(out_rows + 4 * rl) = o;
-          else if constexpr (BF16) *gptr<uint16_t>(out_rows + 2 * rl) = (uint16_t)f32_to_bf16(o);
-          else *gptr<_Float16>(out_rows + 2 * rl) = (_Float16)o;
+        for (int e = 0; e < 4; ++e) {
+          const int t = 4 * q4 + e;
+          const bool tok = t < n;
+          const int tc = tok ? t : 0;
+          const float pv = acc[e] * sc;
+          const float w = Act::ld(vbuf, tc * RPW + rl) - fac[tc].x * pv;
+          wv[e] = tok ? w : 0.f;
+          o_part = (t == n) ? fmaf(lam_all, pv, o_part) : o_part;
         }
       }
-      // C: S_n^T tiles sn[mm][ct] of block mm (ct = 4 hh + w): D row 4 q4 + e
-      // of tile ct is column 64 hh + 16 q4 + 4 w + e, and row l16 of K^T tile
-      // ct (the A operand of lane l) holds that column ordering already. Both
-      // blocks of the vblock stay in registers for the amax and the
-      // requantisation (the reference quantiser, ref:36-37,83-99: s =
-      // amax/448, 1 when amax is not > 0; codes = e4m3fn(clamp(x / s, +-448))
-      // with the unrounded fp32 s; the quotient by quotient_rn when the block
-      // is finite).
-      f32x4_t sn[2][8];
-      uint32_t am = 0;
+      if (n >= LP) {
+        // a full ring: the q row is a block of its own (every row of it is S_0 q)
+        const f32x4_t acc = x_times_s0([&](int by) { return f.lds_q + by; });
+        if (q4 == 0) o_part = fmaf(lam_all, acc[0] * sc, o_part);
+      }
+      // B: U^T = R W^T (fp32 MFMA, contraction index q4 <-> token 4 q4 + e)
+      uint4 packed;
+      {
+        f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+        const float* rrow = Rj + l16 * LP + 4 * q4;
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(rrow[0], wv[0], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(rrow[1], wv[1], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(rrow[2], wv[2], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(rrow[3], wv[3], acc, 0, 0, 0);
+        float ut[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float4 fc = fac[4 * q4 + e];
+          ut[e] = acc[e] * fc.y;
+          o_part = fmaf(ut[e], fc.z, o_part);
+        }
+        if constexpr (BF16) {
+          // hi/lo split: U~ = hi + lo to ~16 bits, both halves bf16 MFMA operands
+          const uint32_t h01 = pack_bf16x2(ut[0], ut[1]), h23 = pack_bf16x2(ut[2], ut[3]);
+          const uint32_t l01 =
+              pack_bf16x2(ut[0] - __uint_as_float(h01 << 16), ut[1] - __uint_as_float(h01 & 0xFFFF0000u));
+          const uint32_t l23 =
+              pack_bf16x2(ut[2] - __uint_as_float(h23 << 16), ut[3] - __uint_as_float(h23 & 0xFFFF0000u));
+          packed = make_uint4(h01, h23, l01, l23);
+        } else {
+          packed = make_uint4(__float_as_uint(ut[0]), __float_as_uint(ut[1]), __float_as_uint(ut[2]),
+                              __float_as_uint(ut[3]));
+        }
+      }
+      o_part += __shfl_xor(o_part, 16);
+      o_part += __shfl_xor(o_part, 32);
+      if (q4 == 0) {
+        const float o = o_part * f.out_scale;
+        if constexpr (ES == 4) *gptr<float>(out_rows + 4 * rl) = o;
+        else if constexpr (BF16) *gptr<uint16_t>(out_rows + 2 * rl) = (uint16_t)f32_to_bf16(o);
+        else *gptr<_Float16>(out_rows + 2 * rl) = (_Float16)o;
+      }
+      // C: S_n^T tiles sn[ct] (ct = 4 hh + w): D row 4 q4 + e of tile ct is
+      // column 64 hh + 16 q4 + 4 w + e, and row l16 of K^T tile ct (the A
+      // operand of lane l) holds that column ordering already.
       // bf16: lam_all scale S_0^T enters through the MFMA as (ls I) S_0^T with
       // ls = lam_all * scale split into bf16 hi + lo (relative error 2^-18);
       // lane (l16, q4) supplies row l16, columns 4 q4 + e of the identity
-      bf16x4_t a2hi, a2lo;
+      f32x4_t sn[8];
       if constexpr (BF16) {
         const float ls = lam_all * sc;
         const uint32_t hb = f32_to_bf16(ls);
@@ -382,84 +366,95 @@ __device__ __attribute__((noinline)) void flush_vblocks(
           h4[e] = (short)(diag ? hb : 0u);
           l4[e] = (short)(diag ? lb : 0u);
         }
-        a2hi = bf16x4_t{h4[0], h4[1], h4[2], h4[3]};
-        a2lo = bf16x4_t{l4[0], l4[1], l4[2], l4[3]};
-      }
-#pragma unroll
-      for (int mm = 0; mm < 2; ++mm) {
+        const bf16x4_t a2hi = bf16x4_t{h4[0], h4[1], h4[2], h4[3]};
+        const bf16x4_t a2lo = bf16x4_t{l4[0], l4[1], l4[2], l4[3]};
 #pragma unroll
         for (int ct = 0; ct < 8; ++ct) {
-          const uint4 c = cf[(ct >> 2) * 2 + mm];
-          const uint32_t wd = (ct & 3) == 0 ? c.x : (ct & 3) == 1 ? c.y : (ct & 3) == 2 ? c.z : c.w;
-          float f[4];
-          fp8x4_to_f32(wd, f);
-          if constexpr (BF16) {
-            const bf16x4_t b2 = __builtin_bit_cast(bf16x4_t, make_uint2(pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3])));
-            const f32x4_t z = {0.f, 0.f, 0.f, 0.f};
-            sn[mm][ct] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a2hi, b2, z, 0, 0, 0);
-            sn[mm][ct] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a2lo, b2, sn[mm][ct], 0, 0, 0);
-          } else {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) sn[mm][ct][e] = lam_all * (f[e] * sc);
-          }
+          const uint4 bv = bvs[ct >> 1];
+          const bf16x4_t b2 = __builtin_bit_cast(bf16x4_t, (ct & 1) ? make_uint2(bv.z, bv.w) : make_uint2(bv.x, bv.y));
+          const f32x4_t z = {0.f, 0.f, 0.f, 0.f};
+          sn[ct] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a2hi, b2, z, 0, 0, 0);
+          sn[ct] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a2lo, b2, sn[ct], 0, 0, 0);
         }
-        if (mm == 1 && p + 1 < fp1) load_vb(p + 1, cf);  // the codes of vblock p are consumed
-        const uint4 u = ubuf[mm * 64 + lane];
-        const uint8_t* kt_lane = lds + f.lds_kt + l16 * 16 * ES + 4 * q4 * ES;  // tokens 4 q4 + e
+      } else {
 #pragma unroll
         for (int ct = 0; ct < 8; ++ct) {
-          const uint8_t* ktrow = kt_lane + ct * 256 * ES;
-          if constexpr (BF16) {
-            const bf16x4_t av = __builtin_bit_cast(bf16x4_t, *(const uint2*)ktrow);
-            sn[mm][ct] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(av, __builtin_bit_cast(bf16x4_t, make_uint2(u.x, u.y)),
-                                                                   sn[mm][ct], 0, 0, 0);
-            sn[mm][ct] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(av, __builtin_bit_cast(bf16x4_t, make_uint2(u.z, u.w)),
-                                                                   sn[mm][ct], 0, 0, 0);
-          } else {
-            const float uf[4] = {__uint_as_float(u.x), __uint_as_float(u.y), __uint_as_float(u.z),
-                                 __uint_as_float(u.w)};
+          float fc[4];
+          fp8x4_to_f32(cw[ct], fc);
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-              sn[mm][ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(Act::ld(ktrow, e), uf[e], sn[mm][ct], 0, 0, 0);
-          }
+          for (int e = 0; e < 4; ++e) sn[ct][e] = lam_all * (fc[e] * sc);
         }
-        // |x| max on the bit patterns (NaN propagates like torch.amax); pairs form v_max3
-#pragma unroll
-        for (int ct = 0; ct < 8; ++ct)
-#pragma unroll
-          for (int e = 0; e < 4; e += 2)
-            am = max(am, max(__float_as_uint(sn[mm][ct][e]) & 0x7FFFFFFFu,
-                             __float_as_uint(sn[mm][ct][e + 1]) & 0x7FFFFFFFu));
       }
-      const uint32_t amb = wave_max_u32(am);
+      if constexpr (!(BF16 || F16))
+        if (p + 1 < nvb) load_blk(p + 1);  // the codes of vblock p are consumed
+      const uint8_t* kt_lane = lds + f.lds_kt + l16 * 16 * ES + 4 * q4 * ES;  // tokens 4 q4 + e
+#pragma unroll
+      for (int ct = 0; ct < 8; ++ct) {
+        const uint8_t* ktrow = kt_lane + ct * 256 * ES;
+        if constexpr (BF16) {
+          const bf16x4_t av = __builtin_bit_cast(bf16x4_t, *(const uint2*)ktrow);
+          sn[ct] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
+              av, __builtin_bit_cast(bf16x4_t, make_uint2(packed.x, packed.y)), sn[ct], 0, 0, 0);
+          sn[ct] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
+              av, __builtin_bit_cast(bf16x4_t, make_uint2(packed.z, packed.w)), sn[ct], 0, 0, 0);
+        } else {
+          const float uf[4] = {__uint_as_float(packed.x), __uint_as_float(packed.y), __uint_as_float(packed.z),
+                               __uint_as_float(packed.w)};
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            sn[ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(Act::ld(ktrow, e), uf[e], sn[ct], 0, 0, 0);
+        }
+      }
+      // |x| max of the block: one v_maximum3 per two values (IEEE maximum: NaN
+      // propagates, like torch.amax); |x| bits order like the values, NaN
+      // above every finite value
+      float am = 0.f;
+#pragma unroll
+      for (int ct = 0; ct < 8; ++ct)
+#pragma unroll
+        for (int e = 0; e < 4; e += 2)
+          am = __builtin_elementwise_maximum(__builtin_elementwise_maximum(am, __builtin_fabsf(sn[ct][e])),
+                                             __builtin_fabsf(sn[ct][e + 1]));
+      uint32_t amb = wave_max_u32(__float_as_uint(am));
+      // the vblock amax: this block's and the other wave's (bounded wait: the
+      // other wave posts every vblock before it waits for this one)
+      __hip_atomic_store(xam_mine + p, (int)(amb | 0x80000000u), __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+      uint32_t other = 0;
+      for (int it = 0; it < (1 << 22); ++it) {
+        other = (uint32_t)__builtin_amdgcn_readfirstlane(
+            __hip_atomic_load(xam_other + p, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP));
+        if (other >> 31) break;
+        __builtin_amdgcn_s_sleep(1);
+      }
+      amb = max(amb, other & 0x7FFFFFFFu);
+      // requantisation (the reference quantiser, ref:36-37,83-99: s = amax/448,
+      // 1 when amax is not > 0; codes = e4m3fn(clamp(x / s, +-448)) with the
+      // unrounded fp32 s; the quotient by quotient_rn when the block is finite)
       const float amax = __uint_as_float(amb);
       const float s32 = (amax > 0.0f) ? amax / 448.0f : 1.0f;
       const bool fast = quotient_fast(amb, s32);
       const float rcp = 1.0f / s32;
+      uint8_t* rp = ck_rows + ((32 * p + 16 * mm + l16) * ck_v + 16 * q4);
 #pragma unroll
-      for (int mm = 0; mm < 2; ++mm) {
-        uint8_t* rp = ck_rows + ((16 * (2 * p + mm) + l16) * ck_v + 16 * q4);
+      for (int hh = 0; hh < 2; ++hh) {
+        uint32_t wd[4];
+        if (fast) {
 #pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-          uint32_t wd[4];
-          if (fast) {
-#pragma unroll
-            for (int w = 0; w < 4; ++w) {
-              const f32x4_t& v = sn[mm][4 * hh + w];
-              wd[w] = f32x4_to_fp8(quotient_rn(v[0], s32, rcp), quotient_rn(v[1], s32, rcp),
-                                   quotient_rn(v[2], s32, rcp), quotient_rn(v[3], s32, rcp));
-            }
-          } else {
-#pragma unroll
-            for (int w = 0; w < 4; ++w) {
-              const f32x4_t& v = sn[mm][4 * hh + w];
-              wd[w] = f32x4_to_fp8_ref(v[0] / s32, v[1] / s32, v[2] / s32, v[3] / s32);
-            }
+          for (int w = 0; w < 4; ++w) {
+            const f32x4_t& v = sn[4 * hh + w];
+            wd[w] = f32x4_to_fp8(quotient_rn(v[0], s32, rcp), quotient_rn(v[1], s32, rcp),
+                                 quotient_rn(v[2], s32, rcp), quotient_rn(v[3], s32, rcp));
           }
-          *gptr<u32x4_t>(rp + 64 * hh) = u32x4_t{wd[0], wd[1], wd[2], wd[3]};
+        } else {
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            const f32x4_t& v = sn[4 * hh + w];
+            wd[w] = f32x4_to_fp8_ref(v[0] / s32, v[1] / s32, v[2] / s32, v[3] / s32);
+          }
         }
+        *gptr<u32x4_t>(rp + 64 * hh) = u32x4_t{wd[0], wd[1], wd[2], wd[3]};
       }
-      if (lane == 0)
+      if (mm == 0 && lane == 0)
         *gptr<uint16_t>(scale_hv + (f.sc_row0 + p) * sc_v) = __builtin_bit_cast(uint16_t, (_Float16)s32);
     }
   }
@@ -500,10 +495,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
   // ---- 0. the head leads publish their coefficients through LDS flags -------------
   // flags[j]: head j's coefficients are in LDS; flags[gw + j]: lead j's
   // share of the k ring has landed; flags[2 gw + j]: streamer j's copy of
-  // the v rows is in LDS; then the new token's (gamma, beta) per head
+  // the v rows is in LDS; then the new token's (gamma, beta) per head, then
+  // the flush's amax exchange words (2 kMaxVBlocks per head)
   int* flags = (int*)(lds + a.lds_flag);
   float* newgates = (float*)(flags + 3 * a.gw);
   if (wave == 0 && lane < 3 * a.gw) flags[lane] = 0;
+  if (wave == 0 && lane < 2 * kMaxVBlocks * a.gw) flags[5 * a.gw + lane] = 0;  // flush amax exchange
   GDNR_WAIT_LGKM0();
   __builtin_amdgcn_s_barrier();  // B0, the only workgroup barrier
 
@@ -587,9 +584,6 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
     }
   };
 
-  // vblocks [fp0, fp1) of the head that this wave rebuilds in a flush, and its
-  // U~/W scratch in LDS
-  int fp0 = 0, fp1 = 0, uoff = 0;
   if (__builtin_amdgcn_readfirstlane((int)head_lead) != 0) {
     const int j = j_head;
     typename Act::Pair q_bits{}, k_bits{};
@@ -883,14 +877,13 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
     // the shared q / new k / K^T are in LDS
     __hip_atomic_store(flags + j, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
     if (__builtin_amdgcn_readfirstlane((int)do_flush) == 0) return;
-    // a flush splits the head's vblocks between the two waves of the head:
-    // the lead takes the upper half once the streamer's copy of the v rows
-    // is in LDS (bounded wait: the streamer always raises the flag)
+    // a flush splits every vblock of the head between the two waves of the
+    // head: the lead takes the upper 16 rows once the streamer's copy of the
+    // v rows is in LDS (bounded wait: the streamer always raises the flag)
     for (int it = 0; it < (1 << 22); ++it) {
       if (flag_set(flags + 2 * a.gw + j)) break;
       __builtin_amdgcn_s_sleep(1);
     }
-    fp0 = NVB / 2, fp1 = NVB, uoff = a.lds_u + (a.gw + j) * LP * 192;
   }
 
   // ---- streamer of head j_head ---------------------------------------------------
@@ -1058,13 +1051,14 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
     for (int i = 0; i < NV; ++i) *(u32x4_t*)(vbuf + 16 * (64 * i + lane)) = vch[i];
     __hip_atomic_store(flags + 2 * a.gw + j_head, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
     await_coefficients();
-    fp0 = 0, fp1 = NVB / 2, uoff = a.lds_u + j_head * LP * 192;
   }
 
-  // ---- 7. flush: MFMA rebuild of vblocks [fp0, fp1) of the head, out of line
+  // ---- 7. flush: MFMA rebuild of block 1 (lead) or 0 (streamer) of every
+  // vblock of the head, out of line
   flush_vblocks<Act, NCH>(ck_rows, scale_hv, out_rows, a.ck_v, a.sc_v, (v0 + r0) / kVBlock, a.out_scale, a.lds_k,
-                          a.lds_knew, a.lds_q, a.lds_r, a.lds_fac, a.lds_lam, a.lds_kt, (int32_t)(vbuf - lds), uoff,
-                          j_head, n, pos, fp0, fp1);
+                          a.lds_knew, a.lds_q, a.lds_r, a.lds_fac, a.lds_lam, a.lds_kt, (int32_t)(vbuf - lds),
+                          a.lds_flag + 4 * (5 * a.gw + 2 * kMaxVBlocks * j_head), j_head, n, pos,
+                          head_lead ? 1 : 0, NVB);
   if (__builtin_amdgcn_readfirstlane((int)head_lead) == 0) append_token();
 }
 

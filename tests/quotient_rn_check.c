@@ -1,6 +1,6 @@
 /* CPU check of the quantiser quotient the kernels use (gdnr_device.h,
- * quotient_rn): q = RN(x * RN(1/s)), then two corrections
- * q = fma(fma(-q, s, x), r, q), then the sign of x, must equal the IEEE
+ * quotient_rn): q = RN(x * RN(1/s)), then two corrections with the negated
+ * residual, q = fma(-fma(q, s, -x), r, q), must equal the IEEE
  * quotient x / s bit for bit on the blocks that take it (amax finite,
  * s = amax / 448 >= 2^-64, |x| <= amax). glibc's fmaf is exact, like the
  * GPU's fused multiply-add. Exit status 1 on any mismatch.
@@ -18,9 +18,9 @@ static uint64_t rnd(void) { st ^= st << 13; st ^= st >> 7; st ^= st << 17; retur
 
 static float quotient_rn(float x, float s, float r) {
   float q = x * r;
-  q = fmaf(fmaf(-q, s, x), r, q);
-  q = fmaf(fmaf(-q, s, x), r, q);
-  return copysignf(q, x);
+  q = fmaf(-fmaf(q, s, -x), r, q);
+  q = fmaf(-fmaf(q, s, -x), r, q);
+  return q;
 }
 
 static long mismatches = 0, checked = 0;
