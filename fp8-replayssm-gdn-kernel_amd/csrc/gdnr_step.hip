@@ -243,6 +243,10 @@ __device__ __attribute__((noinline)) void flush_vblocks(
       }
     };
     load_blk(0);
+    // the first codes are waited for here, outside the loop: a load pending
+    // on entry to the loop would make its header wait for every store of the
+    // previous vblock as well
+    GDNR_WAIT_VMCNT(0);
 #pragma unroll 1
     for (int p = 0; p < nvb; ++p) {
       const float sc = f16_bits_to_f32((uint16_t)ld_u16_uniform((const uint16_t*)(scale_hv + (f.sc_row0 + p) * sc_v)));
@@ -352,8 +356,11 @@ __device__ __attribute__((noinline)) void flush_vblocks(
       // column 64 hh + 16 q4 + 4 w + e, and row l16 of K^T tile ct (the A
       // operand of lane l) holds that column ordering already.
       // bf16: lam_all scale S_0^T enters through the MFMA as (ls I) S_0^T with
-      // ls = lam_all * scale split into bf16 hi + lo (relative error 2^-18);
-      // lane (l16, q4) supplies row l16, columns 4 q4 + e of the identity
+      // ls = lam_all * scale split into bf16 hi + lo (relative error 2^-18).
+      // Each hi/lo pair is one 16x16x32 MFMA: lane (l16, q4) supplies k-slots
+      // 8 q4 + j, j < 4 the hi part and j >= 4 the lo part of token / column
+      // 4 q4 + (j & 3) -- (ls_hi I | ls_lo I) against the codes twice, then
+      // (K^T | K^T) against (U~_hi ; U~_lo)
       f32x4_t sn[8];
       if constexpr (BF16) {
         const float ls = lam_all * sc;
@@ -366,15 +373,15 @@ __device__ __attribute__((noinline)) void flush_vblocks(
           h4[e] = (short)(diag ? hb : 0u);
           l4[e] = (short)(diag ? lb : 0u);
         }
-        const bf16x4_t a2hi = bf16x4_t{h4[0], h4[1], h4[2], h4[3]};
-        const bf16x4_t a2lo = bf16x4_t{l4[0], l4[1], l4[2], l4[3]};
+        const bf16x8_t a_ls = __builtin_bit_cast(
+            bf16x8_t, (short __attribute__((ext_vector_type(8)))){h4[0], h4[1], h4[2], h4[3], l4[0], l4[1], l4[2], l4[3]});
 #pragma unroll
         for (int ct = 0; ct < 8; ++ct) {
           const uint4 bv = bvs[ct >> 1];
-          const bf16x4_t b2 = __builtin_bit_cast(bf16x4_t, (ct & 1) ? make_uint2(bv.z, bv.w) : make_uint2(bv.x, bv.y));
+          const uint2 c2 = (ct & 1) ? make_uint2(bv.z, bv.w) : make_uint2(bv.x, bv.y);
           const f32x4_t z = {0.f, 0.f, 0.f, 0.f};
-          sn[ct] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a2hi, b2, z, 0, 0, 0);
-          sn[ct] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a2lo, b2, sn[ct], 0, 0, 0);
+          sn[ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              a_ls, __builtin_bit_cast(bf16x8_t, make_uint4(c2.x, c2.y, c2.x, c2.y)), z, 0, 0, 0);
         }
       } else {
 #pragma unroll
@@ -392,11 +399,9 @@ __device__ __attribute__((noinline)) void flush_vblocks(
       for (int ct = 0; ct < 8; ++ct) {
         const uint8_t* ktrow = kt_lane + ct * 256 * ES;
         if constexpr (BF16) {
-          const bf16x4_t av = __builtin_bit_cast(bf16x4_t, *(const uint2*)ktrow);
-          sn[ct] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
-              av, __builtin_bit_cast(bf16x4_t, make_uint2(packed.x, packed.y)), sn[ct], 0, 0, 0);
-          sn[ct] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
-              av, __builtin_bit_cast(bf16x4_t, make_uint2(packed.z, packed.w)), sn[ct], 0, 0, 0);
+          const uint2 k2 = *(const uint2*)ktrow;
+          sn[ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, make_uint4(k2.x, k2.y, k2.x, k2.y)),
+                                                           __builtin_bit_cast(bf16x8_t, packed), sn[ct], 0, 0, 0);
         } else {
           const float uf[4] = {__uint_as_float(packed.x), __uint_as_float(packed.y), __uint_as_float(packed.z),
                                __uint_as_float(packed.w)};
