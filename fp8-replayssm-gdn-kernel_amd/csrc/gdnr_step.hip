@@ -947,35 +947,22 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
       for (int i = 0; i < NV; ++i) *(u32x4_t*)(vbuf + 16 * (64 * i + lane)) = vch[i];
       __hip_atomic_store(flags + 2 * a.gw + j_head, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
       await_coefficients();
-      // w = sum_t c_t v_t: per-lane partials over the lane's chunks (rows
-      // EPC rc + [0, EPC)), exchanged through LDS (this head's U~ area, unused
-      // by a replay) and summed per output row below
-      const float* part = (const float*)(lds + a.lds_u + j_head * LP * 192);  // [lane][EPC]
-      {
-        float wp[EPC];
+      // w = sum_t c_t v_t of each row this lane emits (rows 64 m + lane for
+      // NBLK >= 4, else 16 (q4 % 2) + l16), from the staged v rows with the
+      // tokens in order: the sum does not depend on block_v
+      constexpr int NOUT = NBLK >= 4 ? NBLK / 4 : 1;
+      float wrow[NOUT];
 #pragma unroll
-        for (int e = 0; e < EPC; ++e) wp[e] = 0.f;
+      for (int m = 0; m < NOUT; ++m) {
+        const int row = NBLK >= 4 ? 64 * m + lane : 16 * (q4 & 1) + l16;
+        float w = 0.f;
 #pragma unroll
-        for (int i = 0; i < NV; ++i) {
-          const int t = (64 * i + lane) / CPT_V;
-          const bool live = t < n;
-          const float ct = live ? c_head[live ? t : 0] : 0.f;
-          const u32x4_t vc = *(const u32x4_t*)(vbuf + 16 * (64 * i + lane));
-          const uint32_t wd[4] = {vc[0], vc[1], vc[2], vc[3]};
-#pragma unroll
-          for (int w = 0; w < 4; ++w) {
-            if constexpr (ES == 2) {
-              const float2 f = Act::from_pair(wd[w]);
-              wp[2 * w] = fmaf(ct, live ? f.x : 0.f, wp[2 * w]);
-              wp[2 * w + 1] = fmaf(ct, live ? f.y : 0.f, wp[2 * w + 1]);
-            } else {
-              wp[w] = fmaf(ct, live ? __uint_as_float(wd[w]) : 0.f, wp[w]);
-            }
-          }
+        for (int t = 0; t < LP; ++t) {
+          // slots at or past the fill hold stale data: selected away, never summed
+          const float wt = fmaf(c_head[t], Act::ld(vbuf, t * RPW + row), w);
+          w = t < n ? wt : w;
         }
-#pragma unroll
-        for (int e = 0; e < EPC; e += 4)
-          *(float4*)(part + lane * EPC + e) = make_float4(wp[e], wp[e + 1], wp[e + 2], wp[e + 3]);
+        wrow[m] = w;
       }
       // lane (l16, q4) holds, per block i, row 16 i + l16 at columns
       // 64 hh + 16 q4 + [0, 16): partial dots, then a 4-lane butterfly over q4;
@@ -1022,7 +1009,6 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
         const float keep = hi1 ? P[2 * m + 1] : P[2 * m];
         R2[m] = keep + __shfl_xor(send, 16);
       }
-      constexpr int NOUT = NBLK >= 4 ? NBLK / 4 : 1;
 #pragma unroll
       for (int m = 0; m < NOUT; ++m) {
         float tot;
@@ -1042,10 +1028,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
         uint32_t sb = sc_bits[NBLK >= 4 ? 2 * m : 0];
         if constexpr (NBLK >= 4) sb ^= (sb ^ sc_bits[2 * m + 1]) & (0u - (uint32_t)(lane >> 5));
         const float sc = f16_bits_to_f32((uint16_t)sb);
-        float wrow = 0.f;
-#pragma unroll
-        for (int mm = 0; mm < 64 / CPT_V; ++mm) wrow += part[(row / EPC + CPT_V * mm) * EPC + row % EPC];
-        if (NBLK >= 4 || q4 < 2) Act::st(out_rows, row, fmaf(tot, sc, wrow) * a.out_scale);
+        if (NBLK >= 4 || q4 < 2) Act::st(out_rows, row, fmaf(tot, sc, wrow[m]) * a.out_scale);
       }
       append_token();
       return;
