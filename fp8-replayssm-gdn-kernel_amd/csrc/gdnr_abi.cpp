@@ -775,4 +775,48 @@ int gdnr_dequantize_vblock32(const gdnr_tensor* payload, const gdnr_tensor* scal
   return hip_status(gdnr::launch_dequantize(q, stream));
 }
 
+int gdnr_bf16_step(const gdnr_tensor* state, const gdnr_tensor* q, const gdnr_tensor* k, const gdnr_tensor* v,
+                   const gdnr_tensor* g, const gdnr_tensor* beta, const gdnr_tensor* out, void* stream) {
+  g_last_error.clear();
+  GDNR_TRY(check_desc(state, "state", 4));
+  GDNR_TRY(check_dtype(state, "state", {GDNR_DTYPE_BF16, GDNR_DTYPE_F16, GDNR_DTYPE_F32}));
+  const int64_t B = state->shape[0], HV = state->shape[1], V = state->shape[2], K = state->shape[3];
+  if (K != gdnr::kKeyDim)
+    return fail(GDNR_ERR_UNSUPPORTED, "state: K=%lld (only K=%d is built)", (long long)K, gdnr::kKeyDim);
+  if (V % gdnr::kVBlock)
+    return fail(GDNR_ERR_UNSUPPORTED, "state: V=%lld is not a multiple of %d", (long long)V, gdnr::kVBlock);
+  GDNR_TRY(check_inner_unit(state, "state"));
+  GDNR_TRY(check_align(state, "state", 16));
+  const int ses = elem_size(state->dtype);
+  if (state->strides[2] * ses * 32 >= ((int64_t)1 << 31))
+    return fail(GDNR_ERR_UNSUPPORTED, "state: row stride of %lld bytes is too large", (long long)(state->strides[2] * ses));
+  GDNR_TRY(check_desc(k, "k", 3));
+  const int act = k->dtype;
+  if (!is_act(act)) return fail(GDNR_ERR_INVALID_ARGUMENT, "k: dtype %s is not bf16|f16|f32", dtype_name(act));
+  const int64_t H = k->shape[1];
+  if (H <= 0 || HV % H)
+    return fail(GDNR_ERR_INVALID_ARGUMENT, "k: %lld key heads do not divide %lld value heads", (long long)H,
+                (long long)HV);
+  const int es = elem_size(act);
+  GDNR_TRY(check_act_tensor(k, "k", 3, {B, H, K}, act, es));
+  GDNR_TRY(check_act_tensor(q, "q", 3, {B, H, K}, act, es));
+  GDNR_TRY(check_act_tensor(v, "v", 3, {B, HV, V}, act, es));
+  GDNR_TRY(check_act_tensor(g, "g", 2, {B, HV}, act, es));
+  GDNR_TRY(check_act_tensor(beta, "beta", 2, {B, HV}, act, es));
+  GDNR_TRY(check_act_tensor(out, "out", 3, {B, HV, V}, act, es));
+  if (B > 65535) return fail(GDNR_ERR_UNSUPPORTED, "batch %lld exceeds 65535", (long long)B);
+  if (B * HV * V == 0) return GDNR_OK;
+  gdnr::RmwArgs a = {};
+  a.state = state->data, a.st_b = state->strides[0], a.st_h = state->strides[1], a.st_v = state->strides[2];
+  a.q = q->data, a.q_b = q->strides[0], a.q_h = q->strides[1];
+  a.k = k->data, a.k_b = k->strides[0], a.k_h = k->strides[1];
+  a.v = v->data, a.v_b = v->strides[0], a.v_h = v->strides[1];
+  a.g = g->data, a.g_b = g->strides[0], a.g_h = g->strides[1];
+  a.beta = beta->data, a.be_b = beta->strides[0], a.be_h = beta->strides[1];
+  a.out = out->data, a.o_b = out->strides[0], a.o_h = out->strides[1];
+  a.B = (int32_t)B, a.HV = (int32_t)HV, a.V = (int32_t)V, a.G = (int32_t)(HV / H);
+  a.out_scale = 1.0f / __builtin_sqrtf((float)K);
+  return hip_status(gdnr::launch_rmw_step(a, state->dtype, act, stream));
+}
+
 }  // extern "C"

@@ -107,6 +107,20 @@ struct QuantArgs {
   int32_t B, HV, V;
 };
 
+// Full-state read-modify-write decode step (gdnr_rmw.hip). The state
+// strides are in state elements, the others in activation elements.
+struct RmwArgs {
+  void* state; int64_t st_b, st_h, st_v;
+  const void* q; int64_t q_b, q_h;
+  const void* k; int64_t k_b, k_h;
+  const void* v; int64_t v_b, v_h;
+  const void* g; int64_t g_b, g_h;
+  const void* beta; int64_t be_b, be_h;
+  void* out; int64_t o_b, o_h;
+  int32_t B, HV, V, G;
+  float out_scale;
+};
+
 // Launch modes of the replay kernel.
 enum ReplayMode : int { kModeReplay = 0, kModeApply = 1, kModeFused = 2 };
 
@@ -122,6 +136,7 @@ GDNR_DECLARE_LAUNCHERS(f16)
 GDNR_DECLARE_LAUNCHERS(f32)
 #undef GDNR_DECLARE_LAUNCHERS
 int launch_quantize(const QuantArgs& a, void* stream);
+int launch_rmw_step(const RmwArgs& a, int state_dt, int act_dt, void* stream);
 int launch_dequantize(const QuantArgs& a, void* stream);
 const char* hip_error_string(int code);
 

@@ -1,0 +1,160 @@
+// gdnr_rmw.hip -- the full-state read-modify-write decode step on gfx950:
+// the comparator of the ReplaySSM path. One gated delta-rule token per
+// sequence is applied to a state held in full ([B,HV,V,K], bf16/f16/f32),
+// which is read and written back:
+//   S <- e^g S;  r = S k;  S <- S + beta (v - r) k^T;  o = (S q) K^-1/2
+// (the reference's _gdn_bf16_step_kernel, prototype/gdn_replayssm_fp8_kernel.py:245-341,
+// host wrapper gdn_bf16_step :408-450; fp32 arithmetic, the state stored
+// back in its own dtype with round-to-nearest-even, o in the activation dtype).
+//
+// HBM-bound: every state byte is read once and written once; nothing else is
+// larger than a row. A workgroup owns 128 V-rows of one value head (4 waves x
+// 32 rows); a lane owns one 16-byte chunk of a row (8 elements of a 2-byte
+// state, 4 of an f32 one), so a row spans 16 or 32 lanes and each wave
+// instruction moves 4 or 2 whole rows. All of a wave's chunk loads are issued
+// before the first is used; the row dot products reduce across the row's
+// lanes with DPP (plus one swizzle for 32-lane rows).
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "gdnr_device.h"
+#include "gdnr_internal.h"
+
+namespace gdnr {
+namespace {
+
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kRowsPerWave = 32;
+constexpr int kRowsPerBlock = 4 * kRowsPerWave;
+
+// sum over the aligned group of LANES lanes (16 or 32), in every lane of it
+template <int LANES>
+__device__ __forceinline__ float row_sum(float x) {
+  x = sum8(x);
+  x += dpp_f<kDppMirror>(x);
+  if constexpr (LANES == 32) x += __shfl_xor(x, 16);
+  return x;
+}
+
+// 16-byte chunk <-> EPC floats in the state dtype
+template <class S>
+__device__ __forceinline__ void chunk_to_f32(const u32x4_t c, float* f) {
+  const uint32_t w[4] = {c[0], c[1], c[2], c[3]};
+  if constexpr (S::kBytes == 4) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) f[i] = __uint_as_float(w[i]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float2 p = S::from_pair(w[i]);
+      f[2 * i] = p.x;
+      f[2 * i + 1] = p.y;
+    }
+  }
+}
+template <class S>
+__device__ __forceinline__ u32x4_t f32_to_chunk(const float* f) {
+  if constexpr (S::kBytes == 4) {
+    return u32x4_t{__float_as_uint(f[0]), __float_as_uint(f[1]), __float_as_uint(f[2]), __float_as_uint(f[3])};
+  } else {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      uint32_t pair;
+      S::st2(&pair, f[2 * i], f[2 * i + 1]);
+      w[i] = pair;
+    }
+    return u32x4_t{w[0], w[1], w[2], w[3]};
+  }
+}
+
+template <class S, class Act>
+__global__ __launch_bounds__(256) void rmw_step_kernel(const RmwArgs a) {
+  constexpr int ES = S::kBytes;
+  constexpr int EPC = 16 / ES;              // state elements per lane chunk
+  constexpr int LPR = kKeyDim / EPC;        // lanes per row: 16 or 32
+  constexpr int RPI = 64 / LPR;             // rows per wave instruction: 4 or 2
+  constexpr int NI = kRowsPerWave / RPI;    // chunk loads per lane: 8 or 16
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int hv = blockIdx.x, b = blockIdx.y;
+  const int row0 = blockIdx.z * kRowsPerBlock + wave * kRowsPerWave;  // wave-uniform
+  if (row0 >= a.V) return;                  // V % 32 == 0: a wave's rows are all in or all out
+  const int h = hv / a.G;
+  const int cl = lane % LPR, rsub = lane / LPR;
+
+  uint8_t* sbase = (uint8_t*)a.state + (b * a.st_b + hv * a.st_h + (int64_t)row0 * a.st_v) * ES;
+  const uint32_t row_bytes = (uint32_t)(a.st_v * ES);
+  const uint32_t lane_off = (uint32_t)rsub * row_bytes + 16u * (uint32_t)cl;
+  u32x4_t ch[NI];
+#pragma unroll
+  for (int i = 0; i < NI; ++i) ch[i] = *(const u32x4_t*)(sbase + (lane_off + (uint32_t)(i * RPI) * row_bytes));
+
+  // k and q of the key head at this lane's columns, the head's gate and
+  // beta, and the v element of each row this lane touches
+  const uint8_t* kp = (const uint8_t*)a.k + (b * a.k_b + h * a.k_h + EPC * cl) * Act::kBytes;
+  const uint8_t* qp = (const uint8_t*)a.q + (b * a.q_b + h * a.q_h + EPC * cl) * Act::kBytes;
+  float kf[EPC], qf[EPC];
+#pragma unroll
+  for (int e = 0; e < EPC; ++e) {
+    kf[e] = Act::ld(kp, e);
+    qf[e] = Act::ld(qp, e);
+  }
+  const float gamma = expf(Act::ld(a.g, b * a.g_b + hv * a.g_h));
+  const float beta = Act::ld(a.beta, b * a.be_b + hv * a.be_h);
+  const uint8_t* vp = (const uint8_t*)a.v + (b * a.v_b + hv * a.v_h + row0 + rsub) * Act::kBytes;
+  uint8_t* op = (uint8_t*)a.out + (b * a.o_b + hv * a.o_h + row0 + rsub) * Act::kBytes;
+  float vrow[NI];
+#pragma unroll
+  for (int i = 0; i < NI; ++i) vrow[i] = Act::ld(vp, i * RPI);
+
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    float s[EPC];
+    chunk_to_f32<S>(ch[i], s);
+    float r = 0.f;
+#pragma unroll
+    for (int e = 0; e < EPC; ++e) {
+      s[e] *= gamma;
+      r = fmaf(s[e], kf[e], r);
+    }
+    r = row_sum<LPR>(r);
+    const float c = (vrow[i] - r) * beta;
+    float o = 0.f;
+#pragma unroll
+    for (int e = 0; e < EPC; ++e) {
+      s[e] = fmaf(c, kf[e], s[e]);
+      o = fmaf(s[e], qf[e], o);
+    }
+    o = row_sum<LPR>(o);
+    *(u32x4_t*)(sbase + (lane_off + (uint32_t)(i * RPI) * row_bytes)) = f32_to_chunk<S>(s);
+    if (cl == 0) Act::st(op, i * RPI, o * a.out_scale);
+  }
+}
+
+template <class S>
+int launch_for_state(const RmwArgs& a, int act, hipStream_t s) {
+  const dim3 grid(a.HV, a.B, (a.V + kRowsPerBlock - 1) / kRowsPerBlock);
+  switch (act) {
+    case DT_BF16: hipLaunchKernelGGL((rmw_step_kernel<S, ActBF16>), grid, dim3(256), 0, s, a); break;
+    case DT_F16: hipLaunchKernelGGL((rmw_step_kernel<S, ActF16>), grid, dim3(256), 0, s, a); break;
+    case DT_F32: hipLaunchKernelGGL((rmw_step_kernel<S, ActF32>), grid, dim3(256), 0, s, a); break;
+    default: return (int)hipErrorInvalidValue;
+  }
+  return (int)hipGetLastError();
+}
+
+}  // namespace
+
+int launch_rmw_step(const RmwArgs& a, int state_dt, int act_dt, void* stream) {
+  const hipStream_t s = (hipStream_t)stream;
+  switch (state_dt) {
+    case DT_BF16: return launch_for_state<ActBF16>(a, act_dt, s);
+    case DT_F16: return launch_for_state<ActF16>(a, act_dt, s);
+    case DT_F32: return launch_for_state<ActF32>(a, act_dt, s);
+    default: return (int)hipErrorInvalidValue;
+  }
+}
+
+}  // namespace gdnr

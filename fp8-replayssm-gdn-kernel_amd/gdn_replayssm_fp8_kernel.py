@@ -7,6 +7,7 @@ a caller swaps the import and nothing else:
     gdn_replay_fp8        reference :344-405
     gdn_replay_fp8_split  reference :1129-1235
     gdn_prep_ring         reference :710-795
+    gdn_bf16_step         reference :408-450 (the bf16 read-modify-write comparator)
 
 plus the checkpoint constructors callers take from the reference's
 gdn_replay_fp8_reference.py (QuantizedCheckpoint / quantize_checkpoint /
@@ -39,6 +40,7 @@ __all__ = [
     "gdn_replay_fp8_split",
     "gdn_prep_ring",
     "gdn_prep_replay_fp8",
+    "gdn_bf16_step",
 ]
 
 FP8_DTYPE = torch.float8_e4m3fn
@@ -265,4 +267,25 @@ def gdn_prep_replay_fp8(
                       [mixed_qkv, a, b, a_log.float(), dt_bias.float(), _as_i32(pos), checkpoint, checkpoint_scale,
                        q_out, k_ring, v_ring, g_ring, beta_ring, _as_i32(valid_len), _as_flag(flush), output],
                       [block_v], gdnr_lib.current_stream(device))
+    return output
+
+
+def gdn_bf16_step(
+    state: torch.Tensor,
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    g: torch.Tensor,
+    beta: torch.Tensor,
+) -> torch.Tensor:
+    """One gated delta-rule token on a state held in full, updated in place
+    (reference kernel:408-450, device work :245-341): S <- exp(g) S;
+    r = S k; S <- S + beta (v - r) k^T; returns (S q) K^-1/2 as [B,HV,V] in
+    q's dtype. state [B,HV,V,K] (bf16, f16 or f32); q, k [B,H,K];
+    v [B,HV,V]; g, beta [B,HV] -- views with unit inner stride are taken as
+    they are (the reference passes ring slices, bench_gdn_replayssm.py:278-287)."""
+    device = _require_cuda(state=state, q=q, k=k, v=v, g=g, beta=beta)
+    output = torch.empty(state.shape[0], state.shape[1], state.shape[2], dtype=q.dtype, device=device)
+    with torch.cuda.device(device):
+        gdnr_lib.call("gdnr_bf16_step", [state, q, k, v, g, beta, output], [], gdnr_lib.current_stream(device))
     return output

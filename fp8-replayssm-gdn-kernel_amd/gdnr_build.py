@@ -33,7 +33,8 @@ DEVICE_FLAGS = [
 ]
 HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra"]
 ACTS = ("bf16", "f16", "f32")  # activation dtypes, one kernel object each (GDNR_ACT = index)
-KERNEL_SOURCES = ("gdnr_kernels", "gdnr_step")
+KERNEL_SOURCES = ("gdnr_kernels", "gdnr_step")  # compiled once per activation dtype
+SINGLE_SOURCES = ("gdnr_rmw",)                   # compiled once (dtypes are template arguments)
 
 
 def _run(cmd: list[str], verbose: bool) -> None:
@@ -57,6 +58,10 @@ def build(verbose: bool = False) -> Path:
             obj = BUILD_DIR / f"{src}_{act}.o"
             kern_objs.append(obj)
             jobs.append([HIPCC, *DEVICE_FLAGS, *inc, f"-DGDNR_ACT={i}", "-c", str(CSRC / f"{src}.hip"), "-o", str(obj)])
+    for src in SINGLE_SOURCES:
+        obj = BUILD_DIR / f"{src}.o"
+        kern_objs.append(obj)
+        jobs.append([HIPCC, *DEVICE_FLAGS, *inc, "-c", str(CSRC / f"{src}.hip"), "-o", str(obj)])
     abi_obj = BUILD_DIR / "gdnr_abi.o"
     jobs.append(["g++", *HOST_FLAGS, *inc, "-c", str(CSRC / "gdnr_abi.cpp"), "-o", str(abi_obj)])
     with ThreadPoolExecutor(max_workers=len(jobs)) as pool:

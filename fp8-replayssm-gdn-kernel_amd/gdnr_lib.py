@@ -63,6 +63,7 @@ ENTRY_POINTS = {
     "gdnr_prep_replay_fp8": (16, 1),
     "gdnr_quantize_vblock32": (4, 0),
     "gdnr_dequantize_vblock32": (3, 0),
+    "gdnr_bf16_step": (7, 0),
 }
 
 _lib = None

@@ -174,6 +174,21 @@ int gdnr_quantize_vblock32(const gdnr_tensor* state, const gdnr_tensor* payload,
 int gdnr_dequantize_vblock32(const gdnr_tensor* payload, const gdnr_tensor* scale,
                              const gdnr_tensor* state, void* stream);
 
+/*
+ * The comparator of the ReplaySSM path: one gated delta-rule token per
+ * sequence applied to a state held in full, read and written back in place:
+ *   S <- exp(g) S;  r = S k;  S <- S + beta (v - r) k^T;  out = (S q) K^-1/2
+ * (fp32 arithmetic; S stored back in its own dtype, round-to-nearest-even).
+ * Shapes: state [B,HV,V,K] bf16|f16|f32 (16-byte aligned rows); q, k [B,H,K];
+ *   v [B,HV,V]; g, beta [B,HV]; out [B,HV,V]. q, k, v, g, beta and out share
+ *   one dtype (bf16|f16|f32). K == 128, V % 32 == 0, HV % H == 0, B <= 65535.
+ * Replaces gdn_bf16_step, prototype/gdn_replayssm_fp8_kernel.py:408-450
+ * (device work: _gdn_bf16_step_kernel, same file :245-341).
+ */
+int gdnr_bf16_step(const gdnr_tensor* state, const gdnr_tensor* q, const gdnr_tensor* k,
+                   const gdnr_tensor* v, const gdnr_tensor* g, const gdnr_tensor* beta,
+                   const gdnr_tensor* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -278,6 +278,30 @@ def baseline_decode(initial_state, q, k, v, g, beta, dtype=np.float32):
     return np.concatenate(outputs, axis=1), state
 
 
+def bf16_rmw_step(state, q, k, v, g, beta, state_dtype="bf16", out_dtype="bf16", dtype=np.float32):
+    """kernel:245-341 (host wrapper kernel:408-450): the full-state
+    read-modify-write comparator. One token per sequence, in the kernel's
+    order and fp32: S *= exp(g); r = sum_K(S k); c = (v - r) beta;
+    S += c k^T; o = sum_K(S q) K^-1/2. S goes back in its storage dtype and
+    o in the output dtype, both rounded to nearest even (round_to).
+    state [B,HV,V,K]; q, k [B,H,K] (shared by the HV/H value heads of a key
+    head); v [B,HV,V]; g, beta [B,HV]. Returns (out, new_state) as float32
+    arrays holding values of those dtypes. Pinned (tests/test_oracle_rmw.py):
+    with f32 storage it is run_kernel's one-token step (ref:155-161); from a
+    zero state it is S = beta v k^T, o = beta v (k . q) K^-1/2; beta = 0 is
+    pure decay; the store rounding is round_to (pinned against torch)."""
+    group = v.shape[1] // k.shape[1]
+    s = np.asarray(state, dtype=dtype)
+    k_t = np.repeat(np.asarray(k, dtype=dtype), group, axis=1)
+    q_t = np.repeat(np.asarray(q, dtype=dtype), group, axis=1)
+    s = s * np.exp(np.asarray(g, dtype=dtype))[..., None, None]
+    retrieved = (s * k_t[:, :, None, :]).sum(axis=-1)
+    correction = (np.asarray(v, dtype=dtype) - retrieved) * np.asarray(beta, dtype=dtype)[..., None]
+    s = s + correction[..., None] * k_t[:, :, None, :]
+    out = (s * q_t[:, :, None, :]).sum(axis=-1) * dtype(k.shape[-1] ** -0.5)
+    return round_to(out, out_dtype), round_to(s, state_dtype)
+
+
 def replay_decode(initial_state, q, k, v, g, beta, window, granularity, tile_size=VBLOCK, dtype=np.float32):
     """ref:189-244. Each token: dequantise the checkpoint, replay the ring
     [ring_start, token] forward from it, emit the last output; when the ring

@@ -184,3 +184,39 @@ def test_python_wrappers_refuse_host_tensors():
                           z(B, dtype=torch.int32), z(B, dtype=torch.bool))
     with pytest.raises(ValueError, match="GPU"):
         gk.quantize_checkpoint(torch.zeros(1, 1, 32, 128))
+
+
+def _rmw_args(B=2, H=2, HV=4, V=128, K=128, state_dt=BF16, act=BF16):
+    return {"state": desc([B, HV, V, K], state_dt), "q": desc([B, H, K], act), "k": desc([B, H, K], act),
+            "v": desc([B, HV, V], act), "g": desc([B, HV], act), "beta": desc([B, HV], act),
+            "out": desc([B, HV, V], act)}
+
+
+def _rmw_call(lib, args):
+    order = ["state", "q", "k", "v", "g", "beta", "out"]
+    rc = lib.gdnr_bf16_step(*[ctypes.byref(args[n]) for n in order], None)
+    return rc, lib.gdnr_last_error().decode()
+
+
+@pytest.mark.parametrize("change,code,needle", [
+    ({"state": desc([2, 4, 128, 64], BF16)}, UNSUPPORTED, "K=64"),
+    ({"state": desc([2, 4, 100, 128], BF16)}, UNSUPPORTED, "V=100"),
+    ({"state": desc([2, 4, 128, 128], I32)}, INVALID, "state"),
+    ({"state": desc([2, 4, 128, 128], BF16, data=FAKE + 2)}, INVALID, "aligned"),
+    ({"q": desc([2, 2, 128], F16)}, INVALID, "q"),
+    ({"v": desc([2, 4, 96], BF16)}, INVALID, "v"),
+    ({"k": desc([2, 3, 128], BF16)}, INVALID, "key heads"),
+    ({"beta": desc([2, 4], BF16, strides=[8, 2])}, INVALID, "innermost"),
+])
+def test_bf16_step_rejects_misuse(lib, change, code, needle):
+    args = _rmw_args()
+    args.update(change)
+    rc, msg = _rmw_call(lib, args)
+    assert rc == code, msg
+    assert needle in msg, msg
+
+
+def test_bf16_step_empty_batch_is_a_no_op(lib):
+    rc, msg = _rmw_call(lib, _rmw_args(B=0))
+    assert rc == OK and msg == ""
+
