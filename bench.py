@@ -72,6 +72,8 @@ def parse_args():
                    help="lockstep: the reference's cycle; mixed: sequence b at ring phase b %% L")
     p.add_argument("--cpu-sample", type=int, default=64, help="batch of the CPU-baseline sample (0: skip)")
     p.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a HIP graph")
+    p.add_argument("--no-rmw", action="store_true",
+                   help="skip the same-box timing of the bf16 read-modify-write comparator")
     p.add_argument("--profile", action="store_true",
                    help="short run for rocprofv3: no CPU baseline, few rounds")
     return p.parse_args()
@@ -283,6 +285,19 @@ def main() -> int:
         },
         "wall_us_per_step": wall * 1e6 / steps,
     }
+    if not args.no_rmw and not args.profile:
+        rmw_us = time_bf16_rmw(shape, device, stream)
+        rmw_bytes = bf16_rmw_bytes(traffic_shape)
+        result["bf16_rmw"] = {
+            "kernel": "rmw_step_kernel<ActBF16, ActBF16>",
+            "us_per_step": round(rmw_us, 4),
+            "bytes_per_step": rmw_bytes,
+            "achieved_GBps": round(rmw_bytes / (rmw_us * 1e-6) / 1e9, 1),
+            "frac": round(rmw_bytes / (rmw_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "replayssm_speedup": round(rmw_us / us_step, 3),
+        }
+        log(f"[bench] bf16 read-modify-write comparator: {rmw_us:.3f} us/step, "
+            f"ReplaySSM {rmw_us / us_step:.2f}x faster")
     if args.cpu_sample > 0 and not args.profile:
         log("[bench] timing the CPU baseline ...")
         result["cpu_baseline"] = cpu_baseline(args, traffic_shape, L)
@@ -293,6 +308,51 @@ def main() -> int:
         calibration_copies(device)
     print(json.dumps(result), flush=True)
     return 0
+
+
+RMW_SETS = 6      # rotating bf16 states: 6 x 67 MB at B=64 exceeds the 256 MB Infinity Cache
+RMW_ROUNDS = 50
+
+
+def time_bf16_rmw(shape, device, stream) -> float:
+    """Same-box timing of the comparator the north star names: the bf16
+    read-modify-write decode step (gdn_bf16_step, one launch per step) on
+    the same layer shape and batch, states rotating over RMW_SETS buffers,
+    captured in a HIP graph and timed with HIP events on its stream.
+    Returns microseconds per step."""
+    import torch
+
+    import gdn_replayssm_fp8_kernel as gk
+    import gdn_replayssm_synth as synth
+
+    gen = synth.generator(7, device)
+    a_log, dt_bias = synth.gating_params(shape, gen, device)
+    q, k, v, g, beta = (x.to(torch.bfloat16) for x in synth.token_inputs(shape, 1, gen, device, a_log, dt_bias))
+    q, k, v, g, beta = q[:, 0].contiguous(), k[:, 0].contiguous(), v[:, 0].contiguous(), g[:, 0].contiguous(), \
+        beta[:, 0].contiguous()
+    states = [0.02 * torch.randn(shape.batch, shape.value_heads, shape.value_dim, shape.key_dim, generator=gen,
+                                 device=device).to(torch.bfloat16) for _ in range(RMW_SETS)]
+
+    def one_round():
+        for st in states:
+            gk.gdn_bf16_step(st, q, k, v, g, beta)
+
+    with torch.cuda.stream(stream):
+        one_round()
+        stream.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            one_round()
+        for _ in range(5):
+            graph.replay()
+        stream.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(RMW_ROUNDS):
+            graph.replay()
+        end.record(stream)
+        end.synchronize()
+    return start.elapsed_time(end) * 1e3 / (RMW_ROUNDS * RMW_SETS)
 
 
 CALIB_BYTES = 64 << 20

@@ -7,13 +7,20 @@
 // host wrapper gdn_bf16_step :408-450; fp32 arithmetic, the state stored
 // back in its own dtype with round-to-nearest-even, o in the activation dtype).
 //
+// The state update keeps the reference's order and roundings (S' = e^g S
+// elementwise, r = S' k, S = S' + c k with c = (v - r) beta); the output uses
+// S q = S' q + c (k . q), so its two row sums (S' k and S' q) are reduced
+// together -- equal to the reference's sum of (S q) up to fp32 rounding.
+//
 // HBM-bound: every state byte is read once and written once; nothing else is
-// larger than a row. A workgroup owns 128 V-rows of one value head (4 waves x
-// 32 rows); a lane owns one 16-byte chunk of a row (8 elements of a 2-byte
-// state, 4 of an f32 one), so a row spans 16 or 32 lanes and each wave
-// instruction moves 4 or 2 whole rows. All of a wave's chunk loads are issued
-// before the first is used; the row dot products reduce across the row's
-// lanes with DPP (plus one swizzle for 32-lane rows).
+// larger than a row. A wave owns 32 V-rows of one value head; a lane owns one
+// 16-byte chunk of a row (8 elements of a 2-byte state, 4 of an f32 one), so
+// a row spans 16 or 32 lanes and each wave instruction moves 4 or 2 whole
+// rows. All of a wave's chunk loads are issued before the first is used; each
+// row's store follows its compute while later rows are still arriving. The
+// row sums reduce across the row's lanes with DPP (plus one swizzle for
+// 32-lane rows). Measured on MI355X at the C1 shape: within 15% of an in-place
+// load/store kernel with the same access pattern and no arithmetic.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -24,9 +31,6 @@ namespace gdnr {
 namespace {
 
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-
-constexpr int kRowsPerWave = 32;
-constexpr int kRowsPerBlock = 4 * kRowsPerWave;
 
 // sum over the aligned group of LANES lanes (16 or 32), in every lane of it
 template <int LANES>
@@ -69,18 +73,21 @@ __device__ __forceinline__ u32x4_t f32_to_chunk(const float* f) {
   }
 }
 
-template <class S, class Act>
+// RPW V-rows of one value head per wave, four waves per workgroup over
+// consecutive rows of a sequence's [HV, V] row space
+template <class S, class Act, int RPW>
 __global__ __launch_bounds__(256) void rmw_step_kernel(const RmwArgs a) {
   constexpr int ES = S::kBytes;
   constexpr int EPC = 16 / ES;              // state elements per lane chunk
   constexpr int LPR = kKeyDim / EPC;        // lanes per row: 16 or 32
   constexpr int RPI = 64 / LPR;             // rows per wave instruction: 4 or 2
-  constexpr int NI = kRowsPerWave / RPI;    // chunk loads per lane: 8 or 16
+  constexpr int NI = RPW / RPI;             // chunk loads per lane
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int hv = blockIdx.x, b = blockIdx.y;
-  const int row0 = blockIdx.z * kRowsPerBlock + wave * kRowsPerWave;  // wave-uniform
-  if (row0 >= a.V) return;                  // V % 32 == 0: a wave's rows are all in or all out
+  const int b = blockIdx.y;
+  const int flat = (blockIdx.x * 4 + wave) * RPW;  // first row in the sequence's [HV, V] rows
+  if (flat >= a.HV * a.V) return;                  // wave-uniform
+  const int hv = flat / a.V, row0 = flat - hv * a.V;
   const int h = hv / a.G;
   const int cl = lane % LPR, rsub = lane / LPR;
 
@@ -105,41 +112,46 @@ __global__ __launch_bounds__(256) void rmw_step_kernel(const RmwArgs a) {
   const float beta = Act::ld(a.beta, b * a.be_b + hv * a.be_h);
   const uint8_t* vp = (const uint8_t*)a.v + (b * a.v_b + hv * a.v_h + row0 + rsub) * Act::kBytes;
   uint8_t* op = (uint8_t*)a.out + (b * a.o_b + hv * a.o_h + row0 + rsub) * Act::kBytes;
-  float vrow[NI];
-#pragma unroll
-  for (int i = 0; i < NI; ++i) vrow[i] = Act::ld(vp, i * RPI);
 
+  float kq = 0.f;
+#pragma unroll
+  for (int e = 0; e < EPC; ++e) kq = fmaf(kf[e], qf[e], kq);
+  kq = row_sum<LPR>(kq);
 #pragma unroll
   for (int i = 0; i < NI; ++i) {
     float s[EPC];
     chunk_to_f32<S>(ch[i], s);
-    float r = 0.f;
+    float r = 0.f, sq = 0.f;
 #pragma unroll
     for (int e = 0; e < EPC; ++e) {
       s[e] *= gamma;
       r = fmaf(s[e], kf[e], r);
+      sq = fmaf(s[e], qf[e], sq);
     }
     r = row_sum<LPR>(r);
-    const float c = (vrow[i] - r) * beta;
-    float o = 0.f;
+    sq = row_sum<LPR>(sq);
+    const float c = (Act::ld(vp, i * RPI) - r) * beta;
 #pragma unroll
-    for (int e = 0; e < EPC; ++e) {
-      s[e] = fmaf(c, kf[e], s[e]);
-      o = fmaf(s[e], qf[e], o);
-    }
-    o = row_sum<LPR>(o);
+    for (int e = 0; e < EPC; ++e) s[e] = fmaf(c, kf[e], s[e]);
+    const float o = fmaf(c, kq, sq);
     *(u32x4_t*)(sbase + (lane_off + (uint32_t)(i * RPI) * row_bytes)) = f32_to_chunk<S>(s);
     if (cl == 0) Act::st(op, i * RPI, o * a.out_scale);
   }
 }
 
+template <class S, class Act>
+void launch_rows(const RmwArgs& a, hipStream_t s) {
+  const int rows = a.HV * a.V;  // V % 32 == 0: a wave's rows stay in one head
+  const dim3 grid((rows + 4 * 32 - 1) / (4 * 32), a.B);
+  hipLaunchKernelGGL((rmw_step_kernel<S, Act, 32>), grid, dim3(256), 0, s, a);
+}
+
 template <class S>
 int launch_for_state(const RmwArgs& a, int act, hipStream_t s) {
-  const dim3 grid(a.HV, a.B, (a.V + kRowsPerBlock - 1) / kRowsPerBlock);
   switch (act) {
-    case DT_BF16: hipLaunchKernelGGL((rmw_step_kernel<S, ActBF16>), grid, dim3(256), 0, s, a); break;
-    case DT_F16: hipLaunchKernelGGL((rmw_step_kernel<S, ActF16>), grid, dim3(256), 0, s, a); break;
-    case DT_F32: hipLaunchKernelGGL((rmw_step_kernel<S, ActF32>), grid, dim3(256), 0, s, a); break;
+    case DT_BF16: launch_rows<S, ActBF16>(a, s); break;
+    case DT_F16: launch_rows<S, ActF16>(a, s); break;
+    case DT_F32: launch_rows<S, ActF32>(a, s); break;
     default: return (int)hipErrorInvalidValue;
   }
   return (int)hipGetLastError();
