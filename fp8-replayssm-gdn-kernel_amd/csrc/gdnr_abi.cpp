@@ -281,13 +281,15 @@ bool step_offsets_fit(const gdnr::ReplayArgs& a, int es) {
   if (!pairs) return false;
   const int64_t lim = (int64_t)1 << 31;
   const int64_t B = a.B, L = a.L, HV = a.HV, H = a.H, V = a.V, K = gdnr::kKeyDim;
+  const int64_t S = a.slot ? a.n_slots : B;  // rows of the checkpoint, scale and rings
   auto fits = [lim](int64_t extent_bytes) { return extent_bytes >= 0 && extent_bytes < lim; };
-  bool ok = fits(((B - 1) * a.ck_b + (HV - 1) * a.ck_h + (V - 1) * a.ck_v + K)) &&
-            fits(2 * ((B - 1) * a.sc_b + (HV - 1) * a.sc_h + (V / gdnr::kVBlock - 1) * a.sc_v + 1)) &&
-            fits(es * ((B - 1) * a.k_b + (L - 1) * a.k_t + (H - 1) * a.k_h + K)) &&
-            fits(es * ((B - 1) * a.v_b + (L - 1) * a.v_t + (HV - 1) * a.v_h + V)) &&
-            fits(es * ((B - 1) * a.g_b + (L - 1) * a.g_t + (HV - 1) * a.g_h + 1)) &&
-            fits(es * ((B - 1) * a.be_b + (L - 1) * a.be_t + (HV - 1) * a.be_h + 1)) &&
+  bool ok = fits(((S - 1) * a.ck_b + (HV - 1) * a.ck_h + (V - 1) * a.ck_v + K)) &&
+            fits(2 * ((S - 1) * a.sc_b + (HV - 1) * a.sc_h + (V / gdnr::kVBlock - 1) * a.sc_v + 1)) &&
+            fits(es * ((S - 1) * a.k_b + (L - 1) * a.k_t + (H - 1) * a.k_h + K)) &&
+            fits(es * ((S - 1) * a.v_b + (L - 1) * a.v_t + (HV - 1) * a.v_h + V)) &&
+            fits(es * ((S - 1) * a.g_b + (L - 1) * a.g_t + (HV - 1) * a.g_h + 1)) &&
+            fits(es * ((S - 1) * a.be_b + (L - 1) * a.be_t + (HV - 1) * a.be_h + 1)) &&
+            (!a.slot || fits(4 * ((B - 1) * a.sl_s + 1))) &&
             fits(es * ((B - 1) * a.o_b + (HV - 1) * a.o_h + V)) && fits(4 * ((B - 1) * a.vl_s + 1)) &&
             fits((B - 1) * a.fl_s + 4);
   if (a.mixed) {
@@ -341,6 +343,7 @@ gdnr::StepArgs make_step_args(const gdnr::ReplayArgs& r, int es, int gate_es) {
   s.lds_q = r.lds_q, s.lds_knew = r.lds_knew, s.lds_k = r.lds_k, s.lds_flag = r.lds_flag, s.lds_c = r.lds_c;
   s.lds_t = r.lds_t, s.lds_g = r.lds_g, s.lds_v = r.lds_v, s.lds_r = r.lds_r, s.lds_fac = r.lds_fac;
   s.lds_kt = r.lds_kt, s.lds_lam = r.lds_lam, s.lds_u = r.lds_u, s.lds_bytes = r.lds_bytes;
+  s.slot = (const uint8_t*)r.slot, s.sl_s = u32(4 * r.sl_s), s.n_slots = r.n_slots;
   return s;
 }
 
@@ -740,6 +743,54 @@ int gdnr_prep_replay_fp8(const gdnr_tensor* mixed_qkv, const gdnr_tensor* a, con
   }
   GDNR_TRY(fit_lds(&r, elem_size(g.act), true, true));
   return hip_status(launch_replay(r, g.act, gdnr::kModeFused, a->dtype == GDNR_DTYPE_F32, stream));
+}
+
+int gdnr_prep_replay_fp8_slots(const gdnr_tensor* mixed_qkv, const gdnr_tensor* a, const gdnr_tensor* b,
+                               const gdnr_tensor* a_log, const gdnr_tensor* dt_bias, const gdnr_tensor* pos,
+                               const gdnr_tensor* state_indices, const gdnr_tensor* checkpoint,
+                               const gdnr_tensor* checkpoint_scale, const gdnr_tensor* q_out,
+                               const gdnr_tensor* k_ring, const gdnr_tensor* v_ring, const gdnr_tensor* g_ring,
+                               const gdnr_tensor* beta_ring, const gdnr_tensor* valid_len, const gdnr_tensor* flush,
+                               const gdnr_tensor* out, int32_t block_v, void* stream) {
+  g_last_error.clear();
+  Geometry slots;  // the slot-indexed tensors: rows = slots
+  GDNR_TRY(check_ring(k_ring, v_ring, g_ring, beta_ring, &slots, 16));
+  GDNR_TRY(check_checkpoint(checkpoint, checkpoint_scale, slots));
+  GDNR_TRY(check_desc(state_indices, "state_indices", 1));
+  GDNR_TRY(check_dtype(state_indices, "state_indices", {GDNR_DTYPE_I32}));
+  if (slots.B < 1) return fail(GDNR_ERR_INVALID_ARGUMENT, "the slot tensors hold no slot (slot 0 is the null slot)");
+  if (slots.B > INT32_MAX) return fail(GDNR_ERR_UNSUPPORTED, "more than 2^31 slots");
+  Geometry g = slots;  // the per-sequence tensors: rows = batch
+  g.B = state_indices->shape[0];
+  GDNR_TRY(check_act_tensor(q_out, "q_out", 3, {g.B, g.H, g.K}, g.act, 2 * elem_size(g.act)));
+  GDNR_TRY(check_prep_inputs(mixed_qkv, a, b, a_log, dt_bias, pos, g));
+  GDNR_TRY(check_index_vec(valid_len, "valid_len", g.B, false));
+  GDNR_TRY(check_index_vec(flush, "flush", g.B, true));
+  GDNR_TRY(check_act_tensor(out, "out", 3, {g.B, g.HV, g.V}, g.act, 2));
+  GDNR_TRY(check_block_v(block_v, g));
+  if (g.L > gdnr::kStepRing)
+    return fail(GDNR_ERR_UNSUPPORTED, "state_indices: rings of at most %d tokens (got %lld)", gdnr::kStepRing,
+                (long long)g.L);
+  if (g.B == 0) return GDNR_OK;
+  gdnr::ReplayArgs r = {};
+  fill_common(&r, g, block_v);
+  fill_ckpt(&r, checkpoint, checkpoint_scale);
+  fill_ring(&r, k_ring, v_ring, g_ring, beta_ring);
+  fill_prep_inputs(&r, mixed_qkv, a, b, a_log, dt_bias, pos, q_out);
+  r.q = q_out->data;
+  r.q_b = q_out->strides[0];
+  r.q_h = q_out->strides[1];
+  fill_index(valid_len, &r.valid_len, &r.vl_s);
+  fill_index(flush, &r.flush, &r.fl_s);
+  fill_index(state_indices, &r.slot, &r.sl_s);
+  r.n_slots = (int32_t)slots.B;
+  r.out = out->data;
+  r.o_b = out->strides[0];
+  r.o_h = out->strides[1];
+  if (!step_offsets_fit(r, elem_size(g.act)))
+    return fail(GDNR_ERR_UNSUPPORTED, "state_indices: the slot tensors must span less than 2 GiB each");
+  GDNR_TRY(fit_step(&r, elem_size(g.act)));
+  return hip_status(launch_step(r, g.act, true, a->dtype == GDNR_DTYPE_F32, stream));
 }
 
 int gdnr_quantize_vblock32(const gdnr_tensor* state, const gdnr_tensor* payload, const gdnr_tensor* scale,

@@ -59,8 +59,10 @@ struct ReplayArgs {
   int32_t sw, rpw, lds_knew, lds_flag, lds_c, lds_g;
   // flush (MFMA rebuild), per head: R = (I + M)^-1 [16 x 16] f32, per-token
   // factors (pre, post, dq, -) f32, lam_all f32; K^T operand tiles [K x 16]
-  // in the ring dtype; per wave U~^T and W^T operand tiles (3 KiB)
+  // in the ring dtype; per-head scratch (3 KiB)
   int32_t lds_r, lds_fac, lds_kt, lds_lam, lds_u;
+  // slot indirection of the fused step (see StepArgs); slot == nullptr: none
+  const int32_t* slot; int64_t sl_s; int32_t n_slots;
 };
 
 constexpr int32_t kMaxStepLds = 160 * 1024;  // gfx950 LDS per workgroup
@@ -82,6 +84,10 @@ struct StepArgs {
   int32_t B, H, G, V, L, gw, block_v, n_vt, sw, rpw;
   float out_scale;
   int32_t lds_q, lds_knew, lds_k, lds_flag, lds_c, lds_t, lds_g, lds_v, lds_r, lds_fac, lds_kt, lds_lam, lds_u, lds_bytes;
+  // slot indirection (fused step only): sequence b's checkpoint, scale and
+  // ring rows are those of slot slot[b] (int32, clamped to [0, n_slots));
+  // nullptr: slot b
+  const uint8_t* slot; uint32_t sl_s; int32_t n_slots;
 };
 
 struct PrepArgs {

@@ -465,7 +465,7 @@ __device__ __attribute__((noinline)) void flush_vblocks(
   }
 }
 
-template <class Act, int NCH, bool FUSED, bool GATE_F32>
+template <class Act, int NCH, bool FUSED, bool GATE_F32, bool SLOTS>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void step_kernel(const StepArgs a) {
   constexpr int ES = Act::kBytes;
   constexpr int ROWB = K * ES;          // bytes of one k-ring row
@@ -489,6 +489,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
     vt = blockIdx.x - sub * a.n_vt;
   }
   const int h = blockIdx.y, b = blockIdx.z;
+  // the slot holding sequence b's checkpoint and rings (vLLM's
+  // ssm_state_indices; its load completes at the barrier B0 below)
+  uint32_t slot_raw = 0;
+  if constexpr (SLOTS) slot_raw = ld_u32_uniform(a.slot + b * a.sl_s);
   const int hv0 = h * a.G + sub * a.gw;
   const bool head_lead = wave < a.gw;                  // waves [0, gw): coefficient chains
   const int j_head = head_lead ? wave : wave - a.gw;  // waves [gw, 2 gw): the rows of head j
@@ -508,6 +512,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
   if (wave == 0 && lane < 2 * kMaxVBlocks * a.gw) flags[5 * a.gw + lane] = 0;  // flush amax exchange
   GDNR_WAIT_LGKM0();
   __builtin_amdgcn_s_barrier();  // B0, the only workgroup barrier
+  int bs = b;  // index of the sequence's checkpoint / ring rows
+  if constexpr (SLOTS) {
+    const int sl = (int)__builtin_amdgcn_readfirstlane((int)slot_raw);
+    bs = (sl >= 0 && sl < a.n_slots) ? sl : 0;  // out of range: the null slot
+  }
 
   // ---- 1. metadata (scalar), requested by every wave at once ----------------------
   const int n_raw = (int)ld_u32_uniform(a.valid_len + b * a.vl_s);
@@ -548,8 +557,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
   // checkpoint rows (replay): ck[hh * NBLK + i] = row 16 i + l16, bytes
   // [64 hh + 16 q4, +16); word w of it holds columns 64 hh + 16 q4 + 4 w + e,
   // at a uniform base per 16-row block + one 32-bit lane offset
-  uint8_t* scale_hv = a.scale + (b * a.sc_b + hv * a.sc_h);
-  uint8_t* ck_rows = a.ckpt + (b * a.ck_b + hv * a.ck_h + (v0 + r0) * a.ck_v);
+  uint8_t* scale_hv = a.scale + (bs * a.sc_b + hv * a.sc_h);
+  uint8_t* ck_rows = a.ckpt + (bs * a.ck_b + hv * a.ck_h + (v0 + r0) * a.ck_v);
   const uint32_t ck_lo = (uint32_t)l16 * a.ck_v + 16 * q4;
   uint8_t* out_rows = a.out + (b * a.o_b + hv * a.o_h + (v0 + r0) * ES);
   // wait for this head's lead (bounded: the lead always publishes)
@@ -570,12 +579,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
         for (int i = 0; i < NV; ++i) {
           const int c = 64 * i + lane;
           if (c / CPT_V == pos)
-            *(u32x4_t*)(a.v + (b * a.v_b + pos * a.v_t + hv * a.v_h + v0 * ES + 16 * (c % CPT_V))) =
+            *(u32x4_t*)(a.v + (bs * a.v_b + pos * a.v_t + hv * a.v_h + v0 * ES + 16 * (c % CPT_V))) =
                 *(const u32x4_t*)(vbuf + 16 * c);
         }
         if (vt == 0 && lane == 0) {
-          Act::st(a.g + (b * a.g_b + pos * a.g_t + hv * a.g_h), 0, newgates[2 * j_head]);
-          Act::st(a.beta + (b * a.be_b + pos * a.be_t + hv * a.be_h), 0, newgates[2 * j_head + 1]);
+          Act::st(a.g + (bs * a.g_b + pos * a.g_t + hv * a.g_h), 0, newgates[2 * j_head]);
+          Act::st(a.beta + (bs * a.be_b + pos * a.be_t + hv * a.be_h), 0, newgates[2 * j_head + 1]);
         }
       }
       if (j_head == 0 && vt == 0 && sub == 0) {
@@ -583,7 +592,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
         Act::st2(a.q_out + (b * a.qo_b + h * a.qo_h + 2 * lane * ES), q2.x, q2.y);
         if (pos >= 0) {
           const float2 k2 = Act::ld2(lds + a.lds_knew + 2 * lane * ES);
-          Act::st2(a.k + (b * a.k_b + pos * a.k_t + h * a.k_h + 2 * lane * ES), k2.x, k2.y);
+          Act::st2(a.k + (bs * a.k_b + pos * a.k_t + h * a.k_h + 2 * lane * ES), k2.x, k2.y);
         }
       }
     }
@@ -596,7 +605,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
     float alog_raw = 0.f, dtb_raw = 0.f;
     typename Act::Bits g_bits = 0, b_bits = 0;
     {
-      const uint8_t* kbase = a.k + (b * a.k_b + h * a.k_h);
+      const uint8_t* kbase = a.k + (bs * a.k_b + h * a.k_h);
       const uint32_t kt_bytes = a.k_t;
       const int nch = L * CPT_K;
       const int share = ((nch + a.gw - 1) / a.gw + 63) / 64 * 64;  // whole DMA instructions
@@ -628,8 +637,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
     }
     {
       const int tl = lane < L ? lane : 0;
-      g_bits = Act::ld_bits(a.g + (b * a.g_b + tl * a.g_t + hv * a.g_h), 0);
-      b_bits = Act::ld_bits(a.beta + (b * a.be_b + tl * a.be_t + hv * a.be_h), 0);
+      g_bits = Act::ld_bits(a.g + (bs * a.g_b + tl * a.g_t + hv * a.g_h), 0);
+      b_bits = Act::ld_bits(a.beta + (bs * a.be_b + tl * a.be_t + hv * a.be_h), 0);
     }
     float q0 = 0.f, q1 = 0.f, k0 = 0.f, k1 = 0.f, gate_new = 0.f, beta_new = 0.f;
     GDNR_WAIT_VMCNT(0);  // this lead's share of the k ring and its small operands landed
@@ -910,7 +919,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
     // the new v from mixed_qkv. Every lane loads: the instruction count is static.
     u32x4_t vch[NV];
     {
-      const uint8_t* vring = a.v + (b * a.v_b + hv * a.v_h + v0 * ES);
+      const uint8_t* vring = a.v + (bs * a.v_b + hv * a.v_h + v0 * ES);
       const uint32_t vt_bytes = a.v_t;
 #pragma unroll
       for (int i = 0; i < NV; ++i) {
@@ -1061,10 +1070,10 @@ using Act = ActF32;
 #define GDNR_SUFFIX(name) name##_f32
 #endif
 
-template <int NCH, bool FUSED, bool GATE_F32>
+template <int NCH, bool FUSED, bool GATE_F32, bool SLOTS = false>
 void launch_step_variant(const StepArgs& a, hipStream_t s) {
   const dim3 grid((unsigned)(a.n_vt * (a.G / a.gw)), (unsigned)a.H, (unsigned)a.B), block((unsigned)(64 * a.sw));
-  auto kernel = step_kernel<Act, NCH, FUSED, GATE_F32>;
+  auto kernel = step_kernel<Act, NCH, FUSED, GATE_F32, SLOTS>;
   if (a.lds_bytes > 64 * 1024) {
     // gfx950 has 160 KiB of LDS per workgroup; dynamic allocations above
     // 64 KiB must be enabled per kernel (idempotent, cheap)
@@ -1078,6 +1087,8 @@ void launch_step_variant(const StepArgs& a, hipStream_t s) {
 template <int NCH>
 void launch_step_nch(const StepArgs& a, bool fused, bool gate_f32, hipStream_t s) {
   if (!fused) launch_step_variant<NCH, false, false>(a, s);
+  else if (a.slot && gate_f32) launch_step_variant<NCH, true, true, true>(a, s);
+  else if (a.slot) launch_step_variant<NCH, true, false, true>(a, s);
   else if (gate_f32) launch_step_variant<NCH, true, true>(a, s);
   else launch_step_variant<NCH, true, false>(a, s);
 }

@@ -251,22 +251,38 @@ def gdn_prep_replay_fp8(
     flush: torch.Tensor,
     block_v: int = 128,
     out: torch.Tensor | None = None,
+    state_indices: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """The full-contract decode step in one launch: exactly
     gdn_prep_ring(...) followed by gdn_replay_fp8(checkpoint, checkpoint_scale,
     q_out, k_ring, v_ring, g_ring, beta_ring, valid_len, flush, block_v),
     as sequenced by the reference's prototype/bench_gdn_full_contract.py:138-154
-    and :246-297, with identical results."""
+    and :246-297, with identical results.
+
+    With state_indices [B] (int32 on the device), the checkpoint, scale and
+    rings are a slot-indexed cache [S, ...] (vLLM's layout, slot 0 the null
+    slot) and batch entry b uses slot state_indices[b]; the other arguments
+    stay per batch entry (gdnr_prep_replay_fp8_slots)."""
     device = _require_cuda(mixed_qkv=mixed_qkv, a=a, b=b, a_log=a_log, dt_bias=dt_bias, pos=pos,
                            checkpoint=checkpoint, checkpoint_scale=checkpoint_scale, q_out=q_out, k_ring=k_ring,
                            v_ring=v_ring, g_ring=g_ring, beta_ring=beta_ring, valid_len=valid_len, flush=flush,
-                           out=out)
-    output = _new_out(q_out, v_ring) if out is None else out
+                           out=out, state_indices=state_indices)
+    batch = mixed_qkv.shape[0]
+    output = (torch.empty(batch, v_ring.shape[2], v_ring.shape[3], dtype=q_out.dtype, device=device)
+              if out is None else out)
     with torch.cuda.device(device):
-        gdnr_lib.call("gdnr_prep_replay_fp8",
-                      [mixed_qkv, a, b, a_log.float(), dt_bias.float(), _as_i32(pos), checkpoint, checkpoint_scale,
-                       q_out, k_ring, v_ring, g_ring, beta_ring, _as_i32(valid_len), _as_flag(flush), output],
-                      [block_v], gdnr_lib.current_stream(device))
+        if state_indices is None:
+            gdnr_lib.call("gdnr_prep_replay_fp8",
+                          [mixed_qkv, a, b, a_log.float(), dt_bias.float(), _as_i32(pos), checkpoint,
+                           checkpoint_scale, q_out, k_ring, v_ring, g_ring, beta_ring, _as_i32(valid_len),
+                           _as_flag(flush), output],
+                          [block_v], gdnr_lib.current_stream(device))
+        else:
+            gdnr_lib.call("gdnr_prep_replay_fp8_slots",
+                          [mixed_qkv, a, b, a_log.float(), dt_bias.float(), _as_i32(pos), _as_i32(state_indices),
+                           checkpoint, checkpoint_scale, q_out, k_ring, v_ring, g_ring, beta_ring,
+                           _as_i32(valid_len), _as_flag(flush), output],
+                          [block_v], gdnr_lib.current_stream(device))
     return output
 
 

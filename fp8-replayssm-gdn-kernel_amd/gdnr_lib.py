@@ -61,6 +61,7 @@ ENTRY_POINTS = {
     "gdnr_replay_fp8_split": (11, 3),
     "gdnr_prep_ring": (11, 1),
     "gdnr_prep_replay_fp8": (16, 1),
+    "gdnr_prep_replay_fp8_slots": (17, 1),
     "gdnr_quantize_vblock32": (4, 0),
     "gdnr_dequantize_vblock32": (3, 0),
     "gdnr_bf16_step": (7, 0),

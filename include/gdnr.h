@@ -155,6 +155,33 @@ int gdnr_prep_replay_fp8(const gdnr_tensor* mixed_qkv, const gdnr_tensor* a,
                          int32_t block_v, void* stream);
 
 /*
+ * gdnr_prep_replay_fp8 over a slot-indexed cache (vLLM's layout): sequence
+ * b's checkpoint, scale and ring rows are those of slot state_indices[b].
+ * checkpoint [S,HV,V,K], checkpoint_scale [S,HV,V/32], k_ring [S,L,H,K],
+ * v_ring [S,L,HV,V], g_ring, beta_ring [S,L,HV] hold S >= 1 slots; slot 0 is
+ * the null slot, which padded batch entries point at (their writes land
+ * there and their outputs are meaningless). state_indices [B] i32 (clamped
+ * on the device to [0, S), out of range -> 0); mixed_qkv, a, b, pos, q_out,
+ * valid_len, flush and out are per batch entry as in gdnr_prep_replay_fp8.
+ * Two batch entries must not name the same non-null slot. L <= 16; each slot
+ * tensor must span less than 2 GiB.
+ * No counterpart in the reference's kernels: the slot contract is the
+ * production op's (initial_state = kv_cache[1] [slots,HV,V,K],
+ * ssm_state_indices with slot 0 the null block), findings.md:35-45, applied
+ * to the full-contract step of prototype/bench_gdn_full_contract.py:113-154.
+ */
+int gdnr_prep_replay_fp8_slots(const gdnr_tensor* mixed_qkv, const gdnr_tensor* a,
+                               const gdnr_tensor* b, const gdnr_tensor* a_log,
+                               const gdnr_tensor* dt_bias, const gdnr_tensor* pos,
+                               const gdnr_tensor* state_indices,
+                               const gdnr_tensor* checkpoint, const gdnr_tensor* checkpoint_scale,
+                               const gdnr_tensor* q_out, const gdnr_tensor* k_ring,
+                               const gdnr_tensor* v_ring, const gdnr_tensor* g_ring,
+                               const gdnr_tensor* beta_ring, const gdnr_tensor* valid_len,
+                               const gdnr_tensor* flush, const gdnr_tensor* out,
+                               int32_t block_v, void* stream);
+
+/*
  * vblock32 quantiser, bit-exact with the reference's
  *   scale = fp16(amax/448) if amax > 0 else 1;  codes = e4m3fn(clamp(x/scale, +-448))
  * state [B,HV,V,K] f32 -> payload [B,HV,V,K] fp8|u8, scale [B,HV,V/32] f16|f32.

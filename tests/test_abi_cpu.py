@@ -220,3 +220,39 @@ def test_bf16_step_empty_batch_is_a_no_op(lib):
     rc, msg = _rmw_call(lib, _rmw_args(B=0))
     assert rc == OK and msg == ""
 
+
+def _slots_args(S=3, B=2, L=4, H=2, HV=4, K=128, V=128, idx_dt=I32):
+    return [desc([B, 2 * H * K + HV * V], BF16), desc([B, HV], BF16), desc([B, HV], BF16), desc([HV], F32),
+            desc([HV], F32), desc([B], I32), desc([B], idx_dt), desc([S, HV, V, K], FP8),
+            desc([S, HV, V // 32], F16), desc([B, H, K], BF16), desc([S, L, H, K], BF16),
+            desc([S, L, HV, V], BF16), desc([S, L, HV], BF16), desc([S, L, HV], BF16), desc([B], I32),
+            desc([B], BOOL), desc([B, HV, V], BF16)]
+
+
+def _slots_call(lib, args, block_v=128):
+    rc = lib.gdnr_prep_replay_fp8_slots(*[ctypes.byref(t) for t in args], block_v, None)
+    return rc, lib.gdnr_last_error().decode()
+
+
+@pytest.mark.parametrize("kwargs,code,needle", [
+    ({"L": 32}, UNSUPPORTED, "at most 16"),
+    ({"idx_dt": I64}, INVALID, "state_indices"),
+    ({"S": 0}, INVALID, "null slot"),
+])
+def test_slots_step_rejects_misuse(lib, kwargs, code, needle):
+    rc, msg = _slots_call(lib, _slots_args(**kwargs))
+    assert rc == code, msg
+    assert needle in msg, msg
+
+
+def test_slots_step_batch_shape_is_checked(lib):
+    args = _slots_args()
+    args[16] = desc([3, 4, 128], BF16)  # out with 3 rows for a batch of 2
+    rc, msg = _slots_call(lib, args)
+    assert rc == INVALID and "out" in msg
+
+
+def test_slots_step_empty_batch_is_a_no_op(lib):
+    rc, msg = _slots_call(lib, _slots_args(B=0))
+    assert rc == OK and msg == ""
+
