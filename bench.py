@@ -74,6 +74,8 @@ def parse_args():
     p.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a HIP graph")
     p.add_argument("--no-rmw", action="store_true",
                    help="skip the same-box timing of the bf16 read-modify-write comparator")
+    p.add_argument("--no-slots", action="store_true",
+                   help="skip the timing of the same cycle through the slot-indexed cache")
     p.add_argument("--profile", action="store_true",
                    help="short run for rocprofv3: no CPU baseline, few rounds")
     return p.parse_args()
@@ -285,6 +287,16 @@ def main() -> int:
         },
         "wall_us_per_step": wall * 1e6 / steps,
     }
+    if not args.no_slots and not args.profile:
+        slot_us = time_slot_path(args, shape, device, stream, ck, mixed, a_raw, b_raw, a_log, dt_bias, meta, rounds,
+                                 warm_rounds)
+        result["slot_indexed"] = {
+            "us_per_step": round(slot_us, 4),
+            "vs_direct": round(slot_us / us_step, 4),
+            "layout": f"checkpoint/rings [{B + 1} slots, ...], slot 0 null, batch entry b in slot perm[b] "
+                      f"(gdnr_prep_replay_fp8_slots)",
+        }
+        log(f"[bench] slot-indexed cycle: {slot_us:.3f} us/step ({slot_us / us_step:.3f}x the direct layout)")
     if not args.no_rmw and not args.profile:
         rmw_us = time_bf16_rmw(shape, device, stream)
         rmw_bytes = bf16_rmw_bytes(traffic_shape)
@@ -308,6 +320,63 @@ def main() -> int:
         calibration_copies(device)
     print(json.dumps(result), flush=True)
     return 0
+
+
+def time_slot_path(args, shape, device, stream, ck, mixed, a_raw, b_raw, a_log, dt_bias, meta, rounds,
+                   warm_rounds) -> float:
+    """The bench cycle again, through the slot-indexed step: every buffer set
+    is a cache of B + 1 slots (slot 0 null) holding the batch at a shuffled
+    slot permutation, the way vLLM's ssm_state_indices address it. Same
+    rounds, graph and event timing as the headline. Returns us per step."""
+    import torch
+
+    import gdn_replayssm_fp8_kernel as gk
+
+    B, L, S = args.batch, args.window, args.sets
+    gen = torch.Generator(device="cpu")
+    gen.manual_seed(3)
+    perm = (torch.randperm(B, generator=gen) + 1).to(torch.int32).to(device)
+    sets = []
+    for _ in range(S):
+        payload = torch.zeros(B + 1, *ck.payload.shape[1:], dtype=ck.payload.dtype, device=device)
+        scale = torch.ones(B + 1, *ck.scale.shape[1:], dtype=ck.scale.dtype, device=device)
+        payload[perm.long()] = ck.payload
+        scale[perm.long()] = ck.scale
+        sets.append(dict(
+            payload=payload, scale=scale,
+            q_out=torch.zeros(B, shape.heads, 128, dtype=torch.bfloat16, device=device),
+            k=torch.zeros(B + 1, L, shape.heads, 128, dtype=torch.bfloat16, device=device),
+            v=torch.zeros(B + 1, L, shape.value_heads, 128, dtype=torch.bfloat16, device=device),
+            g=torch.zeros(B + 1, L, shape.value_heads, dtype=torch.bfloat16, device=device),
+            beta=torch.zeros(B + 1, L, shape.value_heads, dtype=torch.bfloat16, device=device),
+            out=torch.empty(B, shape.value_heads, 128, dtype=torch.bfloat16, device=device)))
+    round_len = S * L
+
+    def one_round():
+        for i in range(round_len):
+            st = sets[i % S]
+            c = (i // S) % L
+            m = meta[c]
+            gk.gdn_prep_replay_fp8(mixed[c], a_raw[c], b_raw[c], a_log, dt_bias, m["pos"], st["payload"],
+                                   st["scale"], st["q_out"], st["k"], st["v"], st["g"], st["beta"], m["valid"],
+                                   m["flush"], block_v=args.block_v, out=st["out"], state_indices=perm)
+
+    with torch.cuda.stream(stream):
+        one_round()
+        stream.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            one_round()
+        for _ in range(warm_rounds):
+            graph.replay()
+        stream.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(rounds):
+            graph.replay()
+        end.record(stream)
+        end.synchronize()
+    return start.elapsed_time(end) * 1e3 / (rounds * round_len)
 
 
 RMW_SETS = 6      # rotating bf16 states: 6 x 67 MB at B=64 exceeds the 256 MB Infinity Cache
