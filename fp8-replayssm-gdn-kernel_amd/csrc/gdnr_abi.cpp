@@ -44,6 +44,7 @@ int elem_size(int dt) {
     case GDNR_DTYPE_I64: return 8;
     case GDNR_DTYPE_FP8E4M3FN:
     case GDNR_DTYPE_U8:
+    case GDNR_DTYPE_I8:
     case GDNR_DTYPE_BOOL: return 1;
     default: return 0;
   }
@@ -56,6 +57,7 @@ const char* dtype_name(int dt) {
     case GDNR_DTYPE_F32: return "f32";
     case GDNR_DTYPE_FP8E4M3FN: return "fp8e4m3fn";
     case GDNR_DTYPE_U8: return "u8";
+    case GDNR_DTYPE_I8: return "i8";
     case GDNR_DTYPE_I32: return "i32";
     case GDNR_DTYPE_I64: return "i64";
     case GDNR_DTYPE_BOOL: return "bool";
@@ -868,6 +870,78 @@ int gdnr_bf16_step(const gdnr_tensor* state, const gdnr_tensor* q, const gdnr_te
   a.B = (int32_t)B, a.HV = (int32_t)HV, a.V = (int32_t)V, a.G = (int32_t)(HV / H);
   a.out_scale = 1.0f / __builtin_sqrtf((float)K);
   return hip_status(gdnr::launch_rmw_step(a, state->dtype, act, stream));
+}
+
+namespace {
+// the scale (or saturated) tensor of a format: shape per granularity, and its
+// [b, hv, i, j] strides
+int check_format_scale(const gdnr_tensor* t, const char* name, int gran, int64_t B, int64_t HV, int64_t V, int64_t K,
+                       int64_t tile, std::initializer_list<int> dtypes, int64_t st[4]) {
+  const bool vb = gran == GDNR_GRANULARITY_VBLOCK;
+  GDNR_TRY(check_desc(t, name, vb ? 3 : 4));
+  GDNR_TRY(check_dtype(t, name, dtypes));
+  if (gran == GDNR_GRANULARITY_HEAD) GDNR_TRY(check_shape(t, name, {B, HV, 1, 1}));
+  else if (gran == GDNR_GRANULARITY_ROW) GDNR_TRY(check_shape(t, name, {B, HV, V, 1}));
+  else if (gran == GDNR_GRANULARITY_TILE) GDNR_TRY(check_shape(t, name, {B, HV, V / tile, K / tile}));
+  else GDNR_TRY(check_shape(t, name, {B, HV, V / tile}));
+  st[0] = t->strides[0], st[1] = t->strides[1], st[2] = t->strides[2], st[3] = vb ? 0 : t->strides[3];
+  return GDNR_OK;
+}
+
+int check_format(const gdnr_tensor* state, const gdnr_tensor* payload, const gdnr_tensor* scale,
+                 const gdnr_tensor* saturated, int32_t gran, int32_t tile, gdnr::FormatArgs* f) {
+  GDNR_TRY(check_desc(state, "state", 4));
+  GDNR_TRY(check_dtype(state, "state", {GDNR_DTYPE_F32}));
+  const int64_t B = state->shape[0], HV = state->shape[1], V = state->shape[2], K = state->shape[3];
+  GDNR_TRY(check_desc(payload, "payload", 4));
+  GDNR_TRY(check_dtype(payload, "payload", {GDNR_DTYPE_FP8E4M3FN, GDNR_DTYPE_U8, GDNR_DTYPE_I8}));
+  GDNR_TRY(check_shape(payload, "payload", {B, HV, V, K}));
+  GDNR_TRY(check_inner_unit(state, "state"));
+  GDNR_TRY(check_inner_unit(payload, "payload"));
+  if (gran < GDNR_GRANULARITY_HEAD || gran > GDNR_GRANULARITY_VBLOCK)
+    return fail(GDNR_ERR_INVALID_ARGUMENT, "granularity %d: expected 0 (head), 1 (row), 2 (tile) or 3 (vblock)",
+                gran);
+  const bool tiled = gran == GDNR_GRANULARITY_TILE || gran == GDNR_GRANULARITY_VBLOCK;
+  if (tiled && (tile < 1 || V % tile || (gran == GDNR_GRANULARITY_TILE && K % tile)))
+    return fail(GDNR_ERR_INVALID_ARGUMENT, "tile_size=%d must divide V=%lld%s", tile, (long long)V,
+                gran == GDNR_GRANULARITY_TILE ? " and K" : "");
+  if (B * HV > INT32_MAX || V > INT32_MAX || K > INT32_MAX)
+    return fail(GDNR_ERR_UNSUPPORTED, "state extents too large");
+  int64_t sc[4], sa[4] = {0, 0, 0, 0};
+  GDNR_TRY(check_format_scale(scale, "scale", gran, B, HV, V, K, tiled ? tile : 1,
+                              {GDNR_DTYPE_F16, GDNR_DTYPE_F32}, sc));
+  if (saturated)
+    GDNR_TRY(check_format_scale(saturated, "saturated", gran, B, HV, V, K, tiled ? tile : 1, {GDNR_DTYPE_I32}, sa));
+  *f = {};
+  f->state = (float*)state->data, f->st_b = state->strides[0], f->st_h = state->strides[1], f->st_v = state->strides[2];
+  f->payload = payload->data, f->pl_b = payload->strides[0], f->pl_h = payload->strides[1];
+  f->pl_v = payload->strides[2];
+  f->scale = scale->data, f->sc_b = sc[0], f->sc_h = sc[1], f->sc_r = sc[2], f->sc_c = sc[3];
+  f->scale_dt = scale->dtype == GDNR_DTYPE_F32 ? gdnr::DT_F32 : gdnr::DT_F16;
+  f->saturated = saturated ? (int32_t*)saturated->data : nullptr;
+  f->sa_b = sa[0], f->sa_h = sa[1], f->sa_r = sa[2], f->sa_c = sa[3];
+  f->B = (int32_t)B, f->HV = (int32_t)HV, f->V = (int32_t)V, f->K = (int32_t)K;
+  f->gran = gran, f->tile = tiled ? tile : 1, f->int8 = payload->dtype == GDNR_DTYPE_I8;
+  return GDNR_OK;
+}
+}  // namespace
+
+int gdnr_quantize_checkpoint(const gdnr_tensor* state, const gdnr_tensor* payload, const gdnr_tensor* scale,
+                             const gdnr_tensor* saturated, int32_t granularity, int32_t tile_size, void* stream) {
+  g_last_error.clear();
+  gdnr::FormatArgs f;
+  GDNR_TRY(check_format(state, payload, scale, saturated, granularity, tile_size, &f));
+  if ((int64_t)f.B * f.HV * f.V * f.K == 0) return GDNR_OK;
+  return hip_status(gdnr::launch_format_quantize(f, stream));
+}
+
+int gdnr_dequantize_checkpoint(const gdnr_tensor* payload, const gdnr_tensor* scale, const gdnr_tensor* state,
+                               int32_t granularity, int32_t tile_size, void* stream) {
+  g_last_error.clear();
+  gdnr::FormatArgs f;
+  GDNR_TRY(check_format(state, payload, scale, nullptr, granularity, tile_size, &f));
+  if ((int64_t)f.B * f.HV * f.V * f.K == 0) return GDNR_OK;
+  return hip_status(gdnr::launch_format_dequantize(f, stream));
 }
 
 }  // extern "C"

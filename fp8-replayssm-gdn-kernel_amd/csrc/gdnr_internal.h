@@ -113,6 +113,19 @@ struct QuantArgs {
   int32_t B, HV, V;
 };
 
+// Checkpoint formats of the reference quantiser (gdnr_formats.hip): scale
+// group granularity, tile size (tile / vblock), fp8 or int8 codes. Strides
+// in elements; the scale and saturated tensors are indexed [b, hv, i, j]
+// (unused trailing strides are 0).
+enum Granularity : int32_t { kGranHead = 0, kGranRow = 1, kGranTile = 2, kGranVblock = 3 };
+struct FormatArgs {
+  float* state; int64_t st_b, st_h, st_v;  // quantise reads it, dequantise writes it
+  void* payload; int64_t pl_b, pl_h, pl_v;
+  void* scale; int64_t sc_b, sc_h, sc_r, sc_c; int32_t scale_dt;
+  int32_t* saturated; int64_t sa_b, sa_h, sa_r, sa_c;  // may be null
+  int32_t B, HV, V, K, gran, tile, int8;
+};
+
 // Full-state read-modify-write decode step (gdnr_rmw.hip). The state
 // strides are in state elements, the others in activation elements.
 struct RmwArgs {
@@ -143,6 +156,8 @@ GDNR_DECLARE_LAUNCHERS(f32)
 #undef GDNR_DECLARE_LAUNCHERS
 int launch_quantize(const QuantArgs& a, void* stream);
 int launch_rmw_step(const RmwArgs& a, int state_dt, int act_dt, void* stream);
+int launch_format_quantize(const FormatArgs& a, void* stream);
+int launch_format_dequantize(const FormatArgs& a, void* stream);
 int launch_dequantize(const QuantArgs& a, void* stream);
 const char* hip_error_string(int code);
 

@@ -88,41 +88,76 @@ class QuantizedCheckpoint:
         return self.payload.numel() * self.payload.element_size() + self.scale.numel() * self.scale.element_size()
 
 
+GRANULARITY_CODES = {"head": 0, "row": 1, "tile": 2, "vblock": 3}
+
+
+def _format(granularity: str) -> tuple[str, int, bool]:
+    is_int8 = granularity.endswith("_int8")
+    base = granularity[: -len("_int8")] if is_int8 else granularity
+    if base not in GRANULARITY_CODES:
+        raise ValueError(f"unsupported granularity: {granularity}")
+    return base, GRANULARITY_CODES[base], is_int8
+
+
+def _scale_shape(base: str, batch: int, heads: int, value_dim: int, key_dim: int, tile_size: int) -> tuple:
+    if base == "head":
+        return (batch, heads, 1, 1)
+    if base == "row":
+        return (batch, heads, value_dim, 1)
+    if base == "tile":
+        return (batch, heads, value_dim // tile_size, key_dim // tile_size)
+    return (batch, heads, value_dim // tile_size)
+
+
 def quantize_checkpoint(state: torch.Tensor, granularity: str = "vblock", tile_size: int = VBLOCK,
                         saturation: bool = True) -> QuantizedCheckpoint:
-    """Device quantiser, bit-exact with ref:40-106 for granularity "vblock",
-    tile_size 32: scale = fp16(amax/448) (1 where amax is not > 0), payload =
-    e4m3fn(clamp(state / (amax/448), +-448)).
+    """Device quantiser, bit-exact with ref:40-106 for every format: granularity
+    "head", "row", "tile" or "vblock" (tile_size for the last two), with
+    "_int8" for int8 codes. Per scale group: scale = fp16(amax/qmax) (1 where
+    amax is not > 0; qmax 448, or 127 for int8); payload = e4m3fn or
+    round-half-even int8 of clamp(state / s), where s is the unrounded
+    amax/qmax for tile and vblock and the fp16 scale for head and row. The
+    decode path reads "vblock"/32 (its own fast quantiser).
 
     ``saturation=False`` skips the host read-back of saturation_fraction
     (which synchronises, like the reference's ``.item()``) and reports 0.
     """
-    if granularity != "vblock" or tile_size != VBLOCK:
-        raise NotImplementedError("the device quantiser builds vblock/32 checkpoints only")
+    base, code, is_int8 = _format(granularity)
     device = _require_cuda(state=state)
     state32 = state if state.dtype == torch.float32 else state.float()
     if state32.dim() != 4:
         raise ValueError("state must be [B, HV, V, K]")
     batch, heads, value_dim, key_dim = state32.shape
-    payload = torch.empty(state32.shape, dtype=FP8_DTYPE, device=device)
-    scale = torch.empty(batch, heads, value_dim // VBLOCK, dtype=torch.float16, device=device)
+    if base in ("tile", "vblock") and (value_dim % tile_size or (base == "tile" and key_dim % tile_size)):
+        raise ValueError(f"{base} granularity requires dimensions divisible by tile_size")
+    payload = torch.empty(state32.shape, dtype=torch.int8 if is_int8 else FP8_DTYPE, device=device)
+    scale = torch.empty(_scale_shape(base, batch, heads, value_dim, key_dim, tile_size), dtype=torch.float16,
+                        device=device)
     saturated = torch.empty(scale.shape, dtype=torch.int32, device=device) if saturation else None
     with torch.cuda.device(device):
-        gdnr_lib.call("gdnr_quantize_vblock32", [state32, payload, scale, saturated],
-                      stream=gdnr_lib.current_stream(device))
+        if base == "vblock" and tile_size == VBLOCK and not is_int8:
+            gdnr_lib.call("gdnr_quantize_vblock32", [state32, payload, scale, saturated],
+                          stream=gdnr_lib.current_stream(device))
+        else:
+            gdnr_lib.call("gdnr_quantize_checkpoint", [state32, payload, scale, saturated], [code, tile_size],
+                          gdnr_lib.current_stream(device))
     fraction = float(saturated.sum().item()) / max(state32.numel(), 1) if saturation else 0.0
-    return QuantizedCheckpoint(payload, scale, "vblock", VBLOCK, fraction)
+    return QuantizedCheckpoint(payload, scale, granularity, tile_size, fraction)
 
 
 def dequantize_checkpoint(checkpoint: QuantizedCheckpoint) -> torch.Tensor:
-    """ref:109-134 for vblock/32 checkpoints: float(payload) * float(scale)."""
-    if checkpoint.granularity != "vblock" or checkpoint.tile_size != VBLOCK:
-        raise NotImplementedError("the device dequantiser reads vblock/32 checkpoints only")
+    """ref:109-134 for every format: float(payload) * float(scale), the scale
+    broadcast over its group."""
+    base, code, _ = _format(checkpoint.granularity)
     device = _require_cuda(payload=checkpoint.payload, scale=checkpoint.scale)
     out = torch.empty(checkpoint.payload.shape, dtype=torch.float32, device=device)
     with torch.cuda.device(device):
-        gdnr_lib.call("gdnr_dequantize_vblock32", [checkpoint.payload, checkpoint.scale, out],
-                      stream=gdnr_lib.current_stream(device))
+        if base == "vblock" and checkpoint.tile_size == VBLOCK and checkpoint.payload.dtype != torch.int8:
+            gdnr_lib.call("gdnr_dequantize_vblock32", [checkpoint.payload, checkpoint.scale, out],
+                          stream=gdnr_lib.current_stream(device))
+        else:
+            gdnr_lib.call("gdnr_dequantize_checkpoint", [checkpoint.payload, checkpoint.scale, out],
+                          [code, checkpoint.tile_size], gdnr_lib.current_stream(device))
     return out
 
 

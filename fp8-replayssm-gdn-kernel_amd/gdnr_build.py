@@ -34,7 +34,7 @@ DEVICE_FLAGS = [
 HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra"]
 ACTS = ("bf16", "f16", "f32")  # activation dtypes, one kernel object each (GDNR_ACT = index)
 KERNEL_SOURCES = ("gdnr_kernels", "gdnr_step")  # compiled once per activation dtype
-SINGLE_SOURCES = ("gdnr_rmw",)                   # compiled once (dtypes are template arguments)
+SINGLE_SOURCES = ("gdnr_rmw", "gdnr_formats")   # compiled once (dtypes are template arguments)
 
 
 def _run(cmd: list[str], verbose: bool) -> None:

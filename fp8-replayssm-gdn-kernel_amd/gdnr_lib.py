@@ -32,6 +32,7 @@ DTYPE_CODES = {
     torch.int32: 5,
     torch.int64: 6,
     torch.bool: 7,
+    torch.int8: 8,
 }
 
 STATUS_NAMES = {1: "invalid argument", 2: "unsupported", 3: "HIP error"}
@@ -65,6 +66,8 @@ ENTRY_POINTS = {
     "gdnr_quantize_vblock32": (4, 0),
     "gdnr_dequantize_vblock32": (3, 0),
     "gdnr_bf16_step": (7, 0),
+    "gdnr_quantize_checkpoint": (4, 2),
+    "gdnr_dequantize_checkpoint": (3, 2),
 }
 
 _lib = None

@@ -44,8 +44,17 @@ typedef enum gdnr_dtype {
   GDNR_DTYPE_U8 = 4,        /* accepted wherever fp8 codes are: raw bytes */
   GDNR_DTYPE_I32 = 5,
   GDNR_DTYPE_I64 = 6,
-  GDNR_DTYPE_BOOL = 7
+  GDNR_DTYPE_BOOL = 7,
+  GDNR_DTYPE_I8 = 8         /* int8 checkpoint codes (the *_int8 formats) */
 } gdnr_dtype;
+
+/* scale-group granularity of a checkpoint format (gdnr_quantize_checkpoint) */
+typedef enum gdnr_granularity {
+  GDNR_GRANULARITY_HEAD = 0,   /* one scale per value head [V, K] */
+  GDNR_GRANULARITY_ROW = 1,    /* one scale per V-row */
+  GDNR_GRANULARITY_TILE = 2,   /* one scale per tile_size x tile_size tile */
+  GDNR_GRANULARITY_VBLOCK = 3  /* one scale per tile_size V-rows x K */
+} gdnr_granularity;
 
 typedef struct gdnr_tensor {
   void* data;                       /* device pointer */
@@ -215,6 +224,33 @@ int gdnr_dequantize_vblock32(const gdnr_tensor* payload, const gdnr_tensor* scal
 int gdnr_bf16_step(const gdnr_tensor* state, const gdnr_tensor* q, const gdnr_tensor* k,
                    const gdnr_tensor* v, const gdnr_tensor* g, const gdnr_tensor* beta,
                    const gdnr_tensor* out, void* stream);
+
+/*
+ * Every checkpoint format of the reference's quantiser: granularity head,
+ * row, tile or vblock (tile_size for the last two), codes fp8 e4m3fn
+ * (payload fp8|u8) or int8 (payload i8, the "*_int8" formats). Per scale
+ * group: s = amax/qmax (qmax 448 or 127), 1 when amax is not > 0; stored
+ * scale fp16(s); codes = clamp(x / s) with the unrounded s for tile and
+ * vblock and the fp16-rounded scale for head and row; fp8 rounds to nearest
+ * even (NaN -> 0x7F|sign), int8 rounds half to even (NaN -> 0).
+ * Shapes: state [B,HV,V,K] f32; payload [B,HV,V,K]; scale f16|f32 (f32 holds
+ * the fp16 values) [B,HV,1,1] head, [B,HV,V,1] row, [B,HV,V/t,K/t] tile,
+ * [B,HV,V/t] vblock; saturated (optional, may be NULL) i32 of the scale's
+ * shape: per group, the count of |x/s| > qmax.
+ * Replaces quantize_checkpoint(state, granularity, tile_size),
+ * prototype/gdn_replay_fp8_reference.py:40-106.
+ */
+int gdnr_quantize_checkpoint(const gdnr_tensor* state, const gdnr_tensor* payload,
+                             const gdnr_tensor* scale, const gdnr_tensor* saturated,
+                             int32_t granularity, int32_t tile_size, void* stream);
+
+/*
+ * state = float(code) * float(scale) for any format of gdnr_quantize_checkpoint.
+ * Replaces dequantize_checkpoint, prototype/gdn_replay_fp8_reference.py:109-134.
+ */
+int gdnr_dequantize_checkpoint(const gdnr_tensor* payload, const gdnr_tensor* scale,
+                               const gdnr_tensor* state, int32_t granularity, int32_t tile_size,
+                               void* stream);
 
 #ifdef __cplusplus
 }
