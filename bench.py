@@ -310,6 +310,17 @@ def main() -> int:
         }
         log(f"[bench] bf16 read-modify-write comparator: {rmw_us:.3f} us/step, "
             f"ReplaySSM {rmw_us / us_step:.2f}x faster")
+        packed_us = time_bf16_packed(shape, device, stream)
+        result["bf16_rmw_packed"] = {
+            "kernel": "rmw_step_kernel<ActBF16, ActBF16, 32, PACKED>",
+            "contract": "production: raw mixed_qkv, q/k norm + gates in the kernel, slot-indexed state, "
+                        "out [B,1,HV,V] (gdnr_bf16_step_packed)",
+            "us_per_step": round(packed_us, 4),
+            "frac": round(rmw_bytes / (packed_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "replayssm_speedup": round(packed_us / us_step, 3),
+        }
+        log(f"[bench] production-contract bf16 comparator: {packed_us:.3f} us/step, "
+            f"ReplaySSM {packed_us / us_step:.2f}x faster")
     if args.cpu_sample > 0 and not args.profile:
         log("[bench] timing the CPU baseline ...")
         result["cpu_baseline"] = cpu_baseline(args, traffic_shape, L)
@@ -405,6 +416,52 @@ def time_bf16_rmw(shape, device, stream) -> float:
     def one_round():
         for st in states:
             gk.gdn_bf16_step(st, q, k, v, g, beta)
+
+    with torch.cuda.stream(stream):
+        one_round()
+        stream.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            one_round()
+        for _ in range(5):
+            graph.replay()
+        stream.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(RMW_ROUNDS):
+            graph.replay()
+        end.record(stream)
+        end.synchronize()
+    return start.elapsed_time(end) * 1e3 / (RMW_ROUNDS * RMW_SETS)
+
+
+def time_bf16_packed(shape, device, stream) -> float:
+    """The comparator in the production operator's contract
+    (gdn_bf16_step_packed: raw mixed_qkv, q/k norm and gates in the kernel,
+    a slot-indexed state, out [B,1,HV,V]) on the same shape and batch: one
+    state tensor of RMW_SETS * B + 1 slots, each launch of a round on its own
+    B slots (a shuffled order), captured in a HIP graph and timed with HIP
+    events on its stream. Returns microseconds per step."""
+    import torch
+
+    import gdn_replayssm_fp8_kernel as gk
+    import gdn_replayssm_synth as synth
+
+    gen = synth.generator(8, device)
+    a_log, dt_bias = synth.gating_params(shape, gen, device)
+    mixed, a, b = synth.raw_step_inputs(shape, 1, gen, device)
+    mixed, a, b = mixed[:, 0].contiguous(), a[:, 0].contiguous(), b[:, 0].contiguous()
+    B = shape.batch
+    state = torch.empty(RMW_SETS * B + 1, shape.value_heads, shape.value_dim, shape.key_dim, dtype=torch.bfloat16,
+                        device=device)
+    state.normal_(0.0, 0.02, generator=gen)
+    perm = torch.randperm(RMW_SETS * B, generator=gen, device=device).to(torch.int32) + 1
+    slot_sets = [perm[i * B:(i + 1) * B].contiguous() for i in range(RMW_SETS)]
+    out = torch.empty(B, 1, shape.value_heads, shape.value_dim, dtype=torch.bfloat16, device=device)
+
+    def one_round():
+        for idx in slot_sets:
+            gk.gdn_bf16_step_packed(mixed, a, b, a_log, dt_bias, state, idx, out=out)
 
     with torch.cuda.stream(stream):
         one_round()

@@ -872,6 +872,67 @@ int gdnr_bf16_step(const gdnr_tensor* state, const gdnr_tensor* q, const gdnr_te
   return hip_status(gdnr::launch_rmw_step(a, state->dtype, act, stream));
 }
 
+int gdnr_bf16_step_packed(const gdnr_tensor* mixed_qkv, const gdnr_tensor* a, const gdnr_tensor* b,
+                          const gdnr_tensor* a_log, const gdnr_tensor* dt_bias, const gdnr_tensor* state,
+                          const gdnr_tensor* state_indices, const gdnr_tensor* out, void* stream) {
+  g_last_error.clear();
+  GDNR_TRY(check_desc(state, "state", 4));
+  GDNR_TRY(check_dtype(state, "state", {GDNR_DTYPE_BF16, GDNR_DTYPE_F16, GDNR_DTYPE_F32}));
+  const int64_t S = state->shape[0], HV = state->shape[1], V = state->shape[2], K = state->shape[3];
+  if (K != gdnr::kKeyDim)
+    return fail(GDNR_ERR_UNSUPPORTED, "state: K=%lld (only K=%d is built)", (long long)K, gdnr::kKeyDim);
+  if (V % gdnr::kVBlock)
+    return fail(GDNR_ERR_UNSUPPORTED, "state: V=%lld is not a multiple of %d", (long long)V, gdnr::kVBlock);
+  if (S < 1) return fail(GDNR_ERR_INVALID_ARGUMENT, "state holds no slot (slot 0 is the null slot)");
+  GDNR_TRY(check_inner_unit(state, "state"));
+  GDNR_TRY(check_align(state, "state", 16));
+  const int ses = elem_size(state->dtype);
+  if (state->strides[2] * ses * 32 >= ((int64_t)1 << 31))
+    return fail(GDNR_ERR_UNSUPPORTED, "state: row stride of %lld bytes is too large", (long long)(state->strides[2] * ses));
+  GDNR_TRY(check_desc(mixed_qkv, "mixed_qkv", 2));
+  const int act = mixed_qkv->dtype;
+  if (!is_act(act)) return fail(GDNR_ERR_INVALID_ARGUMENT, "mixed_qkv: dtype %s is not bf16|f16|f32", dtype_name(act));
+  const int64_t B = mixed_qkv->shape[0], width = mixed_qkv->shape[1];
+  const int64_t hk2 = width - HV * V;
+  if (hk2 <= 0 || hk2 % (2 * K))
+    return fail(GDNR_ERR_INVALID_ARGUMENT, "mixed_qkv: width %lld is not 2 H K + HV V (HV=%lld, V=%lld, K=%lld)",
+                (long long)width, (long long)HV, (long long)V, (long long)K);
+  const int64_t H = hk2 / (2 * K);
+  if (HV % H)
+    return fail(GDNR_ERR_INVALID_ARGUMENT, "%lld key heads do not divide %lld value heads", (long long)H, (long long)HV);
+  GDNR_TRY(check_inner_unit(mixed_qkv, "mixed_qkv"));
+  GDNR_TRY(check_desc(a, "a", 2));
+  GDNR_TRY(check_desc(b, "b", 2));
+  if (a->dtype != b->dtype || (a->dtype != act && a->dtype != GDNR_DTYPE_F32))
+    return fail(GDNR_ERR_INVALID_ARGUMENT, "a/b: dtypes %s/%s (expected both f32 or both %s)", dtype_name(a->dtype),
+                dtype_name(b->dtype), dtype_name(act));
+  GDNR_TRY(check_shape(a, "a", {B, HV}));
+  GDNR_TRY(check_shape(b, "b", {B, HV}));
+  GDNR_TRY(check_desc(a_log, "a_log", 1));
+  GDNR_TRY(check_desc(dt_bias, "dt_bias", 1));
+  GDNR_TRY(check_dtype(a_log, "a_log", {GDNR_DTYPE_F32}));
+  GDNR_TRY(check_dtype(dt_bias, "dt_bias", {GDNR_DTYPE_F32}));
+  GDNR_TRY(check_shape(a_log, "a_log", {HV}));
+  GDNR_TRY(check_shape(dt_bias, "dt_bias", {HV}));
+  GDNR_TRY(check_index_vec(state_indices, "state_indices", B, false));
+  GDNR_TRY(check_act_tensor(out, "out", 4, {B, 1, HV, V}, act, elem_size(act)));
+  if (B > 65535) return fail(GDNR_ERR_UNSUPPORTED, "batch %lld exceeds 65535", (long long)B);
+  if (B * HV * V == 0) return GDNR_OK;
+  gdnr::RmwArgs r = {};
+  r.state = state->data, r.st_b = state->strides[0], r.st_h = state->strides[1], r.st_v = state->strides[2];
+  r.mixed = mixed_qkv->data, r.mx_b = mixed_qkv->strides[0];
+  r.a = a->data, r.a_b = a->strides[0], r.a_h = a->strides[1];
+  r.bgate = b->data, r.bg_b = b->strides[0], r.bg_h = b->strides[1];
+  r.a_log = (const float*)a_log->data, r.al_s = a_log->strides[0];
+  r.dt_bias = (const float*)dt_bias->data, r.db_s = dt_bias->strides[0];
+  r.slot = (const int32_t*)state_indices->data, r.sl_s = state_indices->strides[0];
+  r.out = out->data, r.o_b = out->strides[0], r.o_h = out->strides[2];
+  r.B = (int32_t)B, r.HV = (int32_t)HV, r.V = (int32_t)V, r.G = (int32_t)(HV / H), r.H = (int32_t)H;
+  r.n_slots = (int32_t)S;
+  r.out_scale = 1.0f / __builtin_sqrtf((float)K);
+  return hip_status(gdnr::launch_rmw_packed(r, state->dtype, act, a->dtype == GDNR_DTYPE_F32, stream));
+}
+
 namespace {
 // the scale (or saturated) tensor of a format: shape per granularity, and its
 // [b, hv, i, j] strides

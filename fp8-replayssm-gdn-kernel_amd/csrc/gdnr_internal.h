@@ -138,6 +138,15 @@ struct RmwArgs {
   void* out; int64_t o_b, o_h;
   int32_t B, HV, V, G;
   float out_scale;
+  // production contract (packed decode): q, k, v from the raw mixed_qkv row,
+  // q/k L2 norm and the gates computed in the kernel, the state addressed by
+  // slot[b] (clamped to [0, n_slots)); q, k, v, g, beta above are unused
+  const void* mixed; int64_t mx_b;
+  const void* a; int64_t a_b, a_h;
+  const void* bgate; int64_t bg_b, bg_h;
+  const float* a_log; int64_t al_s;
+  const float* dt_bias; int64_t db_s;
+  const int32_t* slot; int64_t sl_s; int32_t n_slots, H;
 };
 
 // Launch modes of the replay kernel.
@@ -156,6 +165,7 @@ GDNR_DECLARE_LAUNCHERS(f32)
 #undef GDNR_DECLARE_LAUNCHERS
 int launch_quantize(const QuantArgs& a, void* stream);
 int launch_rmw_step(const RmwArgs& a, int state_dt, int act_dt, void* stream);
+int launch_rmw_packed(const RmwArgs& a, int state_dt, int act_dt, bool gate_f32, void* stream);
 int launch_format_quantize(const FormatArgs& a, void* stream);
 int launch_format_dequantize(const FormatArgs& a, void* stream);
 int launch_dequantize(const QuantArgs& a, void* stream);

@@ -7,6 +7,11 @@
 // host wrapper gdn_bf16_step :408-450; fp32 arithmetic, the state stored
 // back in its own dtype with round-to-nearest-even, o in the activation dtype).
 //
+// The packed form takes the production operator's contract instead: the raw
+// mixed_qkv row, q/k L2 norm and the gates in the kernel, a slot-indexed
+// state and out [B, 1, HV, V] (findings.md:35-45) -- the comparator of the
+// full-contract ReplaySSM step.
+//
 // The state update keeps the reference's order and roundings (S' = e^g S
 // elementwise, r = S' k, S = S' + c k with c = (v - r) beta); the output uses
 // S q = S' q + c (k . q), so its two row sums (S' k and S' q) are reduced
@@ -74,8 +79,11 @@ __device__ __forceinline__ u32x4_t f32_to_chunk(const float* f) {
 }
 
 // RPW V-rows of one value head per wave, four waves per workgroup over
-// consecutive rows of a sequence's [HV, V] row space
-template <class S, class Act, int RPW>
+// consecutive rows of a sequence's [HV, V] row space. PACKED: the production
+// contract -- q, k, v from the raw mixed_qkv row, q and k L2-normalised and
+// the gates formed in fp32 here (the formulas of the full-contract prep,
+// kernel:504-562), the state of slot slot[b].
+template <class S, class Act, int RPW, bool PACKED = false, bool GATE_F32 = false>
 __global__ __launch_bounds__(256) void rmw_step_kernel(const RmwArgs a) {
   constexpr int ES = S::kBytes;
   constexpr int EPC = 16 / ES;              // state elements per lane chunk
@@ -90,8 +98,13 @@ __global__ __launch_bounds__(256) void rmw_step_kernel(const RmwArgs a) {
   const int hv = flat / a.V, row0 = flat - hv * a.V;
   const int h = hv / a.G;
   const int cl = lane % LPR, rsub = lane / LPR;
+  int bs = b;  // the state's row of this sequence
+  if constexpr (PACKED) {
+    const int sl = (int)__builtin_amdgcn_readfirstlane((int)*(const uint32_t*)(a.slot + b * a.sl_s));
+    bs = (sl >= 0 && sl < a.n_slots) ? sl : 0;  // out of range: the null slot
+  }
 
-  uint8_t* sbase = (uint8_t*)a.state + (b * a.st_b + hv * a.st_h + (int64_t)row0 * a.st_v) * ES;
+  uint8_t* sbase = (uint8_t*)a.state + (bs * a.st_b + hv * a.st_h + (int64_t)row0 * a.st_v) * ES;
   const uint32_t row_bytes = (uint32_t)(a.st_v * ES);
   const uint32_t lane_off = (uint32_t)rsub * row_bytes + 16u * (uint32_t)cl;
   u32x4_t ch[NI];
@@ -100,17 +113,46 @@ __global__ __launch_bounds__(256) void rmw_step_kernel(const RmwArgs a) {
 
   // k and q of the key head at this lane's columns, the head's gate and
   // beta, and the v element of each row this lane touches
-  const uint8_t* kp = (const uint8_t*)a.k + (b * a.k_b + h * a.k_h + EPC * cl) * Act::kBytes;
-  const uint8_t* qp = (const uint8_t*)a.q + (b * a.q_b + h * a.q_h + EPC * cl) * Act::kBytes;
-  float kf[EPC], qf[EPC];
+  float kf[EPC], qf[EPC], gamma, beta;
+  const uint8_t* vp;
+  if constexpr (PACKED) {
+    const uint8_t* row = (const uint8_t*)a.mixed + (int64_t)b * a.mx_b * Act::kBytes;
+    const uint8_t* qp = row + (h * kKeyDim + EPC * cl) * Act::kBytes;
+    const uint8_t* kp = row + ((a.H + h) * kKeyDim + EPC * cl) * Act::kBytes;
+    float qs = 0.f, ks = 0.f;
 #pragma unroll
-  for (int e = 0; e < EPC; ++e) {
-    kf[e] = Act::ld(kp, e);
-    qf[e] = Act::ld(qp, e);
+    for (int e = 0; e < EPC; ++e) {
+      qf[e] = Act::ld(qp, e);
+      kf[e] = Act::ld(kp, e);
+      qs = fmaf(qf[e], qf[e], qs);
+      ks = fmaf(kf[e], kf[e], ks);
+    }
+    const float qd = sqrtf(row_sum<LPR>(qs) + 1e-6f), kd = sqrtf(row_sum<LPR>(ks) + 1e-6f);
+#pragma unroll
+    for (int e = 0; e < EPC; ++e) {
+      qf[e] = qf[e] / qd;
+      kf[e] = kf[e] / kd;
+    }
+    const float araw = GATE_F32 ? ((const float*)a.a)[b * a.a_b + hv * a.a_h] : Act::ld(a.a, b * a.a_b + hv * a.a_h);
+    const float braw = GATE_F32 ? ((const float*)a.bgate)[b * a.bg_b + hv * a.bg_h]
+                                : Act::ld(a.bgate, b * a.bg_b + hv * a.bg_h);
+    const float x = araw + a.dt_bias[hv * a.db_s];
+    const float sp = x <= 20.0f ? logf(1.0f + expf(x)) : x;
+    gamma = expf(-expf(a.a_log[hv * a.al_s]) * sp);
+    beta = 1.0f / (1.0f + expf(-braw));
+    vp = row + (2 * a.H * kKeyDim + hv * a.V + row0 + rsub) * Act::kBytes;
+  } else {
+    const uint8_t* kp = (const uint8_t*)a.k + (b * a.k_b + h * a.k_h + EPC * cl) * Act::kBytes;
+    const uint8_t* qp = (const uint8_t*)a.q + (b * a.q_b + h * a.q_h + EPC * cl) * Act::kBytes;
+#pragma unroll
+    for (int e = 0; e < EPC; ++e) {
+      kf[e] = Act::ld(kp, e);
+      qf[e] = Act::ld(qp, e);
+    }
+    gamma = expf(Act::ld(a.g, b * a.g_b + hv * a.g_h));
+    beta = Act::ld(a.beta, b * a.be_b + hv * a.be_h);
+    vp = (const uint8_t*)a.v + (b * a.v_b + hv * a.v_h + row0 + rsub) * Act::kBytes;
   }
-  const float gamma = expf(Act::ld(a.g, b * a.g_b + hv * a.g_h));
-  const float beta = Act::ld(a.beta, b * a.be_b + hv * a.be_h);
-  const uint8_t* vp = (const uint8_t*)a.v + (b * a.v_b + hv * a.v_h + row0 + rsub) * Act::kBytes;
   uint8_t* op = (uint8_t*)a.out + (b * a.o_b + hv * a.o_h + row0 + rsub) * Act::kBytes;
 
   float kq = 0.f;
@@ -139,11 +181,11 @@ __global__ __launch_bounds__(256) void rmw_step_kernel(const RmwArgs a) {
   }
 }
 
-template <class S, class Act>
+template <class S, class Act, bool PACKED = false, bool GATE_F32 = false>
 void launch_rows(const RmwArgs& a, hipStream_t s) {
   const int rows = a.HV * a.V;  // V % 32 == 0: a wave's rows stay in one head
   const dim3 grid((rows + 4 * 32 - 1) / (4 * 32), a.B);
-  hipLaunchKernelGGL((rmw_step_kernel<S, Act, 32>), grid, dim3(256), 0, s, a);
+  hipLaunchKernelGGL((rmw_step_kernel<S, Act, 32, PACKED, GATE_F32>), grid, dim3(256), 0, s, a);
 }
 
 template <class S>
@@ -157,7 +199,28 @@ int launch_for_state(const RmwArgs& a, int act, hipStream_t s) {
   return (int)hipGetLastError();
 }
 
+template <class S>
+int launch_packed_for_state(const RmwArgs& a, int act, bool gate_f32, hipStream_t s) {
+  switch (act) {
+    case DT_BF16: gate_f32 ? launch_rows<S, ActBF16, true, true>(a, s) : launch_rows<S, ActBF16, true, false>(a, s); break;
+    case DT_F16: gate_f32 ? launch_rows<S, ActF16, true, true>(a, s) : launch_rows<S, ActF16, true, false>(a, s); break;
+    case DT_F32: launch_rows<S, ActF32, true, true>(a, s); break;
+    default: return (int)hipErrorInvalidValue;
+  }
+  return (int)hipGetLastError();
+}
+
 }  // namespace
+
+int launch_rmw_packed(const RmwArgs& a, int state_dt, int act_dt, bool gate_f32, void* stream) {
+  const hipStream_t s = (hipStream_t)stream;
+  switch (state_dt) {
+    case DT_BF16: return launch_packed_for_state<ActBF16>(a, act_dt, gate_f32, s);
+    case DT_F16: return launch_packed_for_state<ActF16>(a, act_dt, gate_f32, s);
+    case DT_F32: return launch_packed_for_state<ActF32>(a, act_dt, gate_f32, s);
+    default: return (int)hipErrorInvalidValue;
+  }
+}
 
 int launch_rmw_step(const RmwArgs& a, int state_dt, int act_dt, void* stream) {
   const hipStream_t s = (hipStream_t)stream;

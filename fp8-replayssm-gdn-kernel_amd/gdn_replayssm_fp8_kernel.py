@@ -41,6 +41,7 @@ __all__ = [
     "gdn_prep_ring",
     "gdn_prep_replay_fp8",
     "gdn_bf16_step",
+    "gdn_bf16_step_packed",
 ]
 
 FP8_DTYPE = torch.float8_e4m3fn
@@ -340,3 +341,31 @@ def gdn_bf16_step(
     with torch.cuda.device(device):
         gdnr_lib.call("gdnr_bf16_step", [state, q, k, v, g, beta, output], [], gdnr_lib.current_stream(device))
     return output
+
+
+def gdn_bf16_step_packed(
+    mixed_qkv: torch.Tensor,
+    a: torch.Tensor,
+    b: torch.Tensor,
+    a_log: torch.Tensor,
+    dt_bias: torch.Tensor,
+    initial_state: torch.Tensor,
+    ssm_state_indices: torch.Tensor,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """The bf16 read-modify-write comparator in the production operator's
+    contract (findings.md:35-45): q/k L2 norm and gating in the kernel,
+    initial_state [slots, HV, V, K] updated in place at slot
+    ssm_state_indices[b] (slot 0 the null slot), out [B, 1, HV, V]."""
+    device = _require_cuda(mixed_qkv=mixed_qkv, a=a, b=b, a_log=a_log, dt_bias=dt_bias,
+                           initial_state=initial_state, ssm_state_indices=ssm_state_indices, out=out)
+    batch = mixed_qkv.shape[0]
+    if out is None:
+        out = torch.empty(batch, 1, initial_state.shape[1], initial_state.shape[2], dtype=mixed_qkv.dtype,
+                          device=device)
+    with torch.cuda.device(device):
+        gdnr_lib.call("gdnr_bf16_step_packed", [mixed_qkv, a, b, a_log.float(), dt_bias.float(), initial_state,
+                                                _as_i32(ssm_state_indices), out], [],
+                      gdnr_lib.current_stream(device))
+    return out
+

@@ -66,6 +66,7 @@ ENTRY_POINTS = {
     "gdnr_quantize_vblock32": (4, 0),
     "gdnr_dequantize_vblock32": (3, 0),
     "gdnr_bf16_step": (7, 0),
+    "gdnr_bf16_step_packed": (8, 0),
     "gdnr_quantize_checkpoint": (4, 2),
     "gdnr_dequantize_checkpoint": (3, 2),
 }

@@ -226,6 +226,24 @@ int gdnr_bf16_step(const gdnr_tensor* state, const gdnr_tensor* q, const gdnr_te
                    const gdnr_tensor* out, void* stream);
 
 /*
+ * The comparator in the production operator's contract (vLLM's packed GDN
+ * decode): per batch entry b, q, k, v from the raw mixed_qkv row
+ * [q heads | k heads | v heads], q and k L2-normalised (x / sqrt(sum x^2 +
+ * 1e-6)), g = -exp(A_log) softplus_20(a + dt_bias), beta = sigmoid(b), all
+ * in fp32; then the step of gdnr_bf16_step on the state of slot
+ * state_indices[b] (slot 0 the null slot; clamped on the device).
+ * Shapes: mixed_qkv [B, 2*H*K + HV*V]; a, b [B,HV] (f32 or the mixed_qkv
+ * dtype); a_log, dt_bias [HV] f32; state [S,HV,V,K] bf16|f16|f32;
+ * state_indices [B] i32; out [B,1,HV,V] in the mixed_qkv dtype.
+ * The production op's contract is findings.md:35-45; the reference times its
+ * full-contract step against it (prototype/bench_gdn_full_contract.py).
+ */
+int gdnr_bf16_step_packed(const gdnr_tensor* mixed_qkv, const gdnr_tensor* a, const gdnr_tensor* b,
+                          const gdnr_tensor* a_log, const gdnr_tensor* dt_bias,
+                          const gdnr_tensor* state, const gdnr_tensor* state_indices,
+                          const gdnr_tensor* out, void* stream);
+
+/*
  * Every checkpoint format of the reference's quantiser: granularity head,
  * row, tile or vblock (tile_size for the last two), codes fp8 e4m3fn
  * (payload fp8|u8) or int8 (payload i8, the "*_int8" formats). Per scale

@@ -476,6 +476,31 @@ def prep_values(mixed_qkv, a, b, a_log, dt_bias, heads, key_dim, value_heads, va
     return q, k, v, g, beta
 
 
+def packed_rmw_step(state, slots, mixed_qkv, a, b, a_log, dt_bias, heads, state_dtype="bf16", out_dtype="bf16"):
+    """The comparator in the production operator's contract (findings.md:35-45):
+    prep_values (q/k L2 norm, gates; kernel:504-562) then bf16_rmw_step on the
+    state of slot slots[i] of state [S,HV,V,K]. Slots outside [0, S) read slot
+    0. Entries of slot 0 (the null slot, padding) are computed but not stored:
+    the device lets them write the null slot in an unspecified order. The
+    gates and normalised q/k enter the step in float32, as the kernel forms
+    them. Returns (out [B,1,HV,V], new state [S,HV,V,K]) as float32 arrays
+    holding values of the output / storage dtype. Pinned
+    (tests/test_oracle_rmw.py): with slots 1..B in order it is bf16_rmw_step of
+    the prepared values; permuting the batch permutes the outputs and leaves
+    the stored states unchanged; untouched slots keep their bytes."""
+    state = np.asarray(state, dtype=np.float32)
+    value_heads, value_dim, key_dim = state.shape[1:]
+    q, k, v, g, beta = prep_values(mixed_qkv, a, b, a_log, dt_bias, heads, key_dim, value_heads, value_dim)
+    idx = np.asarray(slots, dtype=np.int64)
+    idx = np.where((idx >= 0) & (idx < state.shape[0]), idx, 0)
+    out, new = bf16_rmw_step(state[idx], q.astype(np.float32), k.astype(np.float32), v.astype(np.float32),
+                             g.astype(np.float32), beta.astype(np.float32), state_dtype, out_dtype)
+    result = state.copy()
+    live = idx != 0
+    result[idx[live]] = new[live]
+    return out[:, None], result
+
+
 def prep_ring(mixed_qkv, a, b, a_log, dt_bias, pos, q_out, k_ring, v_ring, g_ring, beta_ring, ring_dtype="bf16", q_dtype=None):
     """kernel:710-795 (gdn_prep_ring): write q_out and ring slot pos[b] of every
     ring, rounding to the storage dtype. Arrays are float32 numpy arrays holding

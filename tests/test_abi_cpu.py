@@ -256,3 +256,38 @@ def test_slots_step_empty_batch_is_a_no_op(lib):
     rc, msg = _slots_call(lib, _slots_args(B=0))
     assert rc == OK and msg == ""
 
+
+
+def _packed_args(S=3, B=2, H=2, HV=4, K=128, V=128, act=BF16, gate=BF16, idx_dt=I32, width=None):
+    return {"mixed": desc([B, width or 2 * H * K + HV * V], act), "a": desc([B, HV], gate),
+            "b": desc([B, HV], gate), "a_log": desc([HV], F32), "dt_bias": desc([HV], F32),
+            "state": desc([S, HV, V, K], BF16), "idx": desc([B], idx_dt), "out": desc([B, 1, HV, V], act)}
+
+
+def _packed_call(lib, args):
+    order = ["mixed", "a", "b", "a_log", "dt_bias", "state", "idx", "out"]
+    rc = lib.gdnr_bf16_step_packed(*[ctypes.byref(args[n]) for n in order], None)
+    return rc, lib.gdnr_last_error().decode()
+
+
+@pytest.mark.parametrize("kwargs,change,code,needle", [
+    ({"width": 2 * 2 * 128 + 4 * 128 + 64}, {}, INVALID, "2 H K + HV V"),
+    ({"H": 3, "width": 2 * 3 * 128 + 4 * 128}, {}, INVALID, "key heads"),
+    ({"gate": F16}, {}, INVALID, "a/b"),
+    ({"idx_dt": I64}, {}, INVALID, "state_indices"),
+    ({"S": 0}, {}, INVALID, "null slot"),
+    ({}, {"out": desc([2, 4, 128], BF16)}, INVALID, "out"),
+    ({}, {"a_log": desc([4], BF16)}, INVALID, "a_log"),
+    ({}, {"state": desc([3, 4, 128, 64], BF16)}, UNSUPPORTED, "K=64"),
+])
+def test_packed_step_rejects_misuse(lib, kwargs, change, code, needle):
+    args = _packed_args(**kwargs)
+    args.update(change)
+    rc, msg = _packed_call(lib, args)
+    assert rc == code, msg
+    assert needle in msg, msg
+
+
+def test_packed_step_empty_batch_is_a_no_op(lib):
+    rc, msg = _packed_call(lib, _packed_args(B=0))
+    assert rc == OK and msg == ""

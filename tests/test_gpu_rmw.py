@@ -84,3 +84,62 @@ def test_rmw_step_two_tokens_in_place(device):
         # continue from the device's own state so that one flipped element does not propagate
         ref_state = np32(state)
         assert rel_l2(np32(out), ref_out) <= 2e-3
+
+
+@pytest.mark.parametrize("state_dtype,act,gate", [(torch.bfloat16, torch.bfloat16, torch.bfloat16),
+                                                  (torch.bfloat16, torch.bfloat16, torch.float32),
+                                                  (torch.float32, torch.float16, torch.float16),
+                                                  (torch.float16, torch.float32, torch.float32)])
+def test_packed_step_matches_oracle(device, state_dtype, act, gate):
+    """The production contract (gdnr_bf16_step_packed): 12 live sequences in
+    out-of-order slots of a 20-slot state plus two padding entries (slot 0),
+    raw mixed_qkv rows, q/k norm and gates in the kernel. Live slots follow
+    the oracle; slots not in the batch keep their bytes; the padding outputs
+    are not checked (they read the null slot)."""
+    B_live, S = 12, 20
+    shape = synth.Shape(B_live)
+    gen = synth.generator(33, device)
+    a_log, dt_bias = synth.gating_params(shape, gen, device)
+    warm = synth.warm_state(synth.Shape(S), 24, gen, device, a_log, dt_bias).to(state_dtype)
+    live_slots = [7, 2, 19, 11, 4, 15, 1, 9, 13, 6, 17, 3]
+    slots = live_slots[:5] + [0] + live_slots[5:] + [0]
+    mixed, a, b = synth.raw_step_inputs(synth.Shape(len(slots)), 1, gen, device, dtype=act, gate_dtype=gate)
+    mixed, a, b = mixed[:, 0].contiguous(), a[:, 0].contiguous(), b[:, 0].contiguous()
+    state = warm.clone()
+    idx = torch.tensor(slots, dtype=torch.int32, device=device)
+    out = gk.gdn_bf16_step_packed(mixed, a, b, a_log, dt_bias, state, idx)
+    ref_out, ref_state = gdn_oracle.packed_rmw_step(np32(warm), slots, np32(mixed), np32(a), np32(b), np32(a_log),
+                                                    np32(dt_bias), shape.heads, STORAGE[state_dtype], STORAGE[act])
+    assert out.shape == (len(slots), 1, shape.value_heads, shape.value_dim) and out.dtype == act
+    live = [i for i, s in enumerate(slots) if s != 0]
+    _check_state(state[live_slots], ref_state[live_slots], state_dtype)
+    untouched = [s for s in range(1, S) if s not in live_slots]
+    assert torch.equal(state[untouched], warm[untouched])
+    assert rel_l2(np32(out)[live], ref_out[live]) <= 2e-3
+
+
+def test_packed_step_equals_the_plain_step_on_prepared_inputs(device):
+    """f32 activations: the packed kernel's in-kernel q/k norm and gates give
+    the plain comparator's result on the same values prepared in f32 on the
+    device (torch), states and outputs within the storage-ulp bound."""
+    shape = synth.Shape(16)
+    gen = synth.generator(34, device)
+    a_log, dt_bias = synth.gating_params(shape, gen, device)
+    warm = synth.warm_state(shape, 16, gen, device, a_log, dt_bias).to(torch.bfloat16)
+    mixed, a, b = synth.raw_step_inputs(shape, 1, gen, device, dtype=torch.float32, gate_dtype=torch.float32)
+    mixed, a, b = mixed[:, 0].contiguous(), a[:, 0].contiguous(), b[:, 0].contiguous()
+    HK = shape.heads * shape.key_dim
+    q = mixed[:, :HK].reshape(16, shape.heads, -1)
+    k = mixed[:, HK:2 * HK].reshape(16, shape.heads, -1)
+    q = q / torch.sqrt((q * q).sum(-1, keepdim=True) + 1e-6)
+    k = k / torch.sqrt((k * k).sum(-1, keepdim=True) + 1e-6)
+    v = mixed[:, 2 * HK:].reshape(16, shape.value_heads, -1).contiguous()
+    g = -torch.exp(a_log) * torch.nn.functional.softplus(a + dt_bias, beta=1.0, threshold=20.0)
+    beta = torch.sigmoid(b)
+    s_plain = torch.cat([warm[:1], warm]).clone()
+    s_packed = s_plain.clone()
+    out_plain = gk.gdn_bf16_step(s_plain[1:], q.contiguous(), k.contiguous(), v, g.contiguous(), beta.contiguous())
+    idx = torch.arange(1, 17, dtype=torch.int32, device=device)
+    out_packed = gk.gdn_bf16_step_packed(mixed, a, b, a_log, dt_bias, s_packed, idx)
+    _check_state(s_packed[1:], np32(s_plain[1:]), torch.bfloat16)
+    assert rel_l2(np32(out_packed[:, 0]), np32(out_plain)) <= 2e-3

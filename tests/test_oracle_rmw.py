@@ -67,3 +67,83 @@ def test_storage_rounding_matches_torch(storage, torch_dtype):
     out, new = gdn_oracle.bf16_rmw_step(state, q, k, v, g, beta, storage, storage)
     np.testing.assert_array_equal(new, torch.from_numpy(new32).to(torch_dtype).float().numpy())
     np.testing.assert_array_equal(out, torch.from_numpy(out32).to(torch_dtype).float().numpy())
+
+
+# --- the production-contract form (gdn_oracle.packed_rmw_step) -------------
+
+S_SLOTS = 5
+
+
+def _packed_inputs(seed=1):
+    rng = np.random.default_rng(seed)
+    mixed = rng.standard_normal((B, 2 * H * K + HV * V)).astype(np.float32)
+    a = rng.standard_normal((B, HV)).astype(np.float32)
+    b = rng.standard_normal((B, HV)).astype(np.float32)
+    a_log = rng.random(HV).astype(np.float32)
+    dt_bias = (rng.random(HV) - 1).astype(np.float32)
+    return mixed, a, b, a_log, dt_bias
+
+
+def test_packed_zero_state_closed_form():
+    """Zero state in slots 3 and 1: S = sigmoid(b) v khat^T and
+    o = sigmoid(b) v (khat . qhat) K^-1/2, with qhat, khat = x / sqrt(|x|^2 +
+    1e-6) and sigmoid from torch; the other slots keep their values."""
+    mixed, a, b, a_log, dt_bias = _packed_inputs()
+    rng = np.random.default_rng(9)
+    state = (0.1 * rng.standard_normal((S_SLOTS, HV, V, K))).astype(np.float32)
+    slots = [3, 1]
+    state[slots] = 0
+    out, new = gdn_oracle.packed_rmw_step(state, slots, mixed, a, b, a_log, dt_bias, H, "f32", "f32")
+    t = torch.from_numpy(mixed).double()
+    q = t[:, :H * K].reshape(B, H, K)
+    k = t[:, H * K:2 * H * K].reshape(B, H, K)
+    q = q / torch.sqrt((q * q).sum(-1, keepdim=True) + 1e-6)
+    k = k / torch.sqrt((k * k).sum(-1, keepdim=True) + 1e-6)
+    v = t[:, 2 * H * K:].reshape(B, HV, V)
+    beta = torch.sigmoid(torch.from_numpy(b).double())
+    kt = k.repeat_interleave(HV // H, dim=1)
+    qt = q.repeat_interleave(HV // H, dim=1)
+    want_s = beta[..., None, None] * v[..., None] * kt[:, :, None, :]
+    want_o = beta[..., None] * v * (kt * qt).sum(-1)[..., None] * K ** -0.5
+    for i, sl in enumerate(slots):
+        np.testing.assert_allclose(new[sl], want_s[i].numpy(), rtol=1e-5, atol=1e-7)
+    np.testing.assert_allclose(out[:, 0], want_o.numpy(), rtol=1e-4, atol=1e-6)
+    for sl in (0, 2, 4):
+        assert np.array_equal(new[sl], state[sl])
+
+
+def test_packed_closed_gate_is_softplus_decay():
+    """b = -200 closes the write (beta ~ 0): the slot's state is only decayed by
+    exp(-exp(A_log) softplus(a + dt_bias)), softplus from torch with threshold
+    20 (a + dt_bias above 20 included)."""
+    mixed, a, b, a_log, dt_bias = _packed_inputs(2)
+    a[0, :2] = 25.0  # past the softplus threshold
+    b[:] = -200.0
+    rng = np.random.default_rng(4)
+    state = (0.1 * rng.standard_normal((S_SLOTS, HV, V, K))).astype(np.float32)
+    _, new = gdn_oracle.packed_rmw_step(state, [2, 4], mixed, a, b, a_log, dt_bias, H, "f32", "f32")
+    x = torch.from_numpy(a).double() + torch.from_numpy(dt_bias).double()
+    gamma = torch.exp(-torch.exp(torch.from_numpy(a_log).double()) *
+                      torch.nn.functional.softplus(x, beta=1.0, threshold=20.0)).numpy()
+    for i, sl in enumerate((2, 4)):
+        np.testing.assert_allclose(new[sl], state[sl] * gamma[i][:, None, None], rtol=1e-5, atol=1e-8)
+
+
+def test_packed_permutation_and_null_slot():
+    """Permuting the batch (with its slots) permutes the outputs and stores the
+    same states; a padding entry (slot 0) and an out-of-range slot write
+    nothing."""
+    rng = np.random.default_rng(5)
+    mixed = rng.standard_normal((4, 2 * H * K + HV * V)).astype(np.float32)
+    a, b = rng.standard_normal((4, HV)).astype(np.float32), rng.standard_normal((4, HV)).astype(np.float32)
+    a_log, dt_bias = rng.random(HV).astype(np.float32), (rng.random(HV) - 1).astype(np.float32)
+    state = (0.1 * rng.standard_normal((S_SLOTS, HV, V, K))).astype(np.float32)
+    slots = np.array([4, 0, 1, 7])
+    out, new = gdn_oracle.packed_rmw_step(state, slots, mixed, a, b, a_log, dt_bias, H)
+    perm = np.array([2, 0, 3, 1])
+    out_p, new_p = gdn_oracle.packed_rmw_step(state, slots[perm], mixed[perm], a[perm], b[perm], a_log, dt_bias, H)
+    assert np.array_equal(out_p, out[perm])
+    assert np.array_equal(new_p, new)
+    for sl in (0, 2, 3):
+        assert np.array_equal(new[sl], state[sl])
+    assert not np.array_equal(new[4], state[4]) and not np.array_equal(new[1], state[1])
