@@ -518,17 +518,22 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
     bs = (sl >= 0 && sl < a.n_slots) ? sl : 0;  // out of range: the null slot
   }
 
-  // ---- 1. metadata (scalar), requested by every wave at once ----------------------
-  const int n_raw = (int)ld_u32_uniform(a.valid_len + b * a.vl_s);
-  int pos_raw = -1;
-  if constexpr (FUSED) pos_raw = (int)ld_u32_uniform(a.pos + b * a.pos_s);
-  // flush flag: the aligned dword holding the byte
+  // ---- 1. metadata (scalar), requested by each wave once its first loads are
+  // out: the lead after its ring requests, the streamer before it waits for
+  // the ring. (Requested before them, a spill of the loaded value into a VGPR
+  // lane would wait for this load ahead of the ring requests.)
+  int n_raw = 0, pos_raw = -1;
   uint32_t flush_word = 0, flush_shift = 0;
-  if (a.flush) {
-    const uintptr_t fa = (uintptr_t)(a.flush + b * a.fl_s);
-    flush_word = ld_u32_uniform((const void*)(fa & ~(uintptr_t)3));
-    flush_shift = 8u * (uint32_t)(fa & 3);
-  }
+  auto request_meta = [&]() {
+    n_raw = (int)ld_u32_uniform(a.valid_len + b * a.vl_s);
+    if constexpr (FUSED) pos_raw = (int)ld_u32_uniform(a.pos + b * a.pos_s);
+    // flush flag: the aligned dword holding the byte
+    if (a.flush) {
+      const uintptr_t fa = (uintptr_t)(a.flush + b * a.fl_s);
+      flush_word = ld_u32_uniform((const void*)(fa & ~(uintptr_t)3));
+      flush_shift = 8u * (uint32_t)(fa & 3);
+    }
+  };
   // per-sequence metadata, read once the wave needs it
   int n = 0, pos = -1;
   bool do_flush = false;
@@ -640,6 +645,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
       g_bits = Act::ld_bits(a.g + (bs * a.g_b + tl * a.g_t + hv * a.g_h), 0);
       b_bits = Act::ld_bits(a.beta + (bs * a.be_b + tl * a.be_t + hv * a.be_h), 0);
     }
+    request_meta();
     float q0 = 0.f, q1 = 0.f, k0 = 0.f, k1 = 0.f, gate_new = 0.f, beta_new = 0.f;
     GDNR_WAIT_VMCNT(0);  // this lead's share of the k ring and its small operands landed
     // (this flag also starts the streamers: the checkpoint stream begins once
@@ -906,6 +912,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
     // flag): the ring requests of the grid reach memory ahead of the checkpoint
     // stream. A replay holds its checkpoint rows in registers; a flush reads
     // them one vblock at a time in section 7 (its registers go to the rebuild).
+    request_meta();
     for (int jj = 0; jj < a.gw; ++jj)
       for (int it = 0; it < (1 << 22); ++it) {
         if (flag_set(flags + a.gw + jj)) break;
