@@ -943,17 +943,17 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
       uint32_t sc_bits[NVB];  // scalar
 #pragma unroll
       for (int p = 0; p < NVB; ++p) sc_bits[p] = ld_u16_uniform((const uint16_t*)(scale_hv + ((v0 + r0) / kVBlock + p) * a.sc_v));
+      // checkpoint rows, row-contiguous: load i covers rows 8 i + [0, 8) of
+      // the wave's rows (1 KB when they are 128 bytes apart); lane l holds row
+      // 8 i + r8 at columns 16 c8 + [0, 16), r8 = l / 8, c8 = l % 8
+      const int r8 = lane >> 3, c8 = lane & 7;
       uint4 ck[NCH];
       GDNR_COMPILER_FENCE();
       {
-        // one uniform base, a 32-bit lane offset per 16-row block
-        const uint32_t rstep = 16u * (uint32_t)a.ck_v;
+        const uint32_t lo = (uint32_t)r8 * (uint32_t)a.ck_v + 16u * (uint32_t)c8;
+        const uint32_t rstep = 8u * (uint32_t)a.ck_v;
 #pragma unroll
-        for (int i = 0; i < NBLK; ++i) {
-          const uint32_t off = ck_lo + (uint32_t)i * rstep;
-#pragma unroll
-          for (int hh = 0; hh < 2; ++hh) ck[hh * NBLK + i] = *(const uint4*)(ck_rows + (off + 64u * hh));
-        }
+        for (int i = 0; i < NCH; ++i) ck[i] = *(const uint4*)(ck_rows + (lo + (uint32_t)i * rstep));
       }
       GDNR_COMPILER_FENCE();
       // the v rows land ahead of the checkpoint rows: copy them to LDS in
@@ -963,14 +963,20 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
       for (int i = 0; i < NV; ++i) *(u32x4_t*)(vbuf + 16 * (64 * i + lane)) = vch[i];
       __hip_atomic_store(flags + 2 * a.gw + j_head, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
       await_coefficients();
-      // w = sum_t c_t v_t of each row this lane emits (rows 64 m + lane for
-      // NBLK >= 4, else 16 (q4 % 2) + l16), from the staged v rows with the
-      // tokens in order: the sum does not depend on block_v
-      constexpr int NOUT = NBLK >= 4 ? NBLK / 4 : 1;
-      float wrow[NOUT];
+      // The 8 lanes of a row group reduce their NCH partial dots by halving
+      // (partners l ^ 7, l ^ 2, l ^ 1 select on bits 2, 1, 0 of c8): value m
+      // of a lane ends as the total of chunk index ibase + m, row
+      // 8 (ibase + m) + r8. With NCH = 4 the last step is a plain sum and the
+      // lanes with c8 odd emit nothing.
+      constexpr int NFIN = NCH >= 8 ? NCH / 8 : 1;
+      const int b0 = c8 & 1, b1 = (c8 >> 1) & 1, b2 = (c8 >> 2) & 1;
+      const int ibase = b2 * (NCH / 2) + b1 * (NCH / 4) + (NCH >= 8 ? b0 * (NCH / 8) : 0);
+      // w = sum_t c_t v_t of each row this lane emits, tokens in order (the
+      // sum does not depend on block_v)
+      float wrow[NFIN];
 #pragma unroll
-      for (int m = 0; m < NOUT; ++m) {
-        const int row = NBLK >= 4 ? 64 * m + lane : 16 * (q4 & 1) + l16;
+      for (int m = 0; m < NFIN; ++m) {
+        const int row = 8 * (ibase + m) + r8;
         float w = 0.f;
 #pragma unroll
         for (int t = 0; t < LP; ++t) {
@@ -980,16 +986,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
         }
         wrow[m] = w;
       }
-      // lane (l16, q4) holds, per block i, row 16 i + l16 at columns
-      // 64 hh + 16 q4 + [0, 16): partial dots, then a 4-lane butterfly over q4;
-      // one half (hh) of the columns at a time: 16 values of T0 in registers
-      float P[NBLK];
-#pragma unroll
-      for (int i = 0; i < NBLK; ++i) P[i] = 0.f;
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        float Tv[16];
-        const float4* tp = (const float4*)(lds + a.lds_t + (j_head * K + 64 * hh + 16 * q4) * 4);
+      // partial dots of the lane's 16 columns with T0
+      float Tv[16];
+      {
+        const float4* tp = (const float4*)(lds + a.lds_t + (j_head * K + 16 * c8) * 4);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const float4 w = tp[i];
@@ -998,53 +998,58 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
           Tv[4 * i + 2] = w.z;
           Tv[4 * i + 3] = w.w;
         }
-#pragma unroll
-        for (int i = 0; i < NBLK; ++i) {
-          const uint4 c = ck[hh * NBLK + i];
-          const uint32_t w4[4] = {c.x, c.y, c.z, c.w};
-          float p = P[i];
-#pragma unroll
-          for (int w = 0; w < 4; ++w) {
-            float f[4];
-            fp8x4_to_f32(w4[w], f);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) p = fmaf(f[e], Tv[4 * w + e], p);
-          }
-          P[i] = p;
-        }
       }
-      // butterfly over q4 (lanes l16 + 16 q4): step 1 (xor 16) keeps the blocks
-      // with i % 2 == q4 % 2, step 2 (xor 32) those with (i / 2) % 2 == q4 / 2, so
-      // lane l ends with the totals of rows 64 m + l (NBLK >= 4), or lanes q4 and
-      // q4 ^ 2 both with row 16 (q4 % 2) + l16 (NBLK = 2)
-      const bool hi1 = (q4 & 1) != 0, hi2 = (q4 & 2) != 0;
-      float R2[NBLK / 2];
+      float P[NCH];
 #pragma unroll
-      for (int m = 0; m < NBLK / 2; ++m) {
-        const float send = hi1 ? P[2 * m] : P[2 * m + 1];
-        const float keep = hi1 ? P[2 * m + 1] : P[2 * m];
-        R2[m] = keep + __shfl_xor(send, 16);
+      for (int i = 0; i < NCH; ++i) {
+        const uint4 c = ck[i];
+        const uint32_t w4[4] = {c.x, c.y, c.z, c.w};
+        float acc = 0.f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          float f[4];
+          fp8x4_to_f32(w4[w], f);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc = fmaf(f[e], Tv[4 * w + e], acc);
+        }
+        P[i] = acc;
+      }
+      // halving steps: keep one half, add the partner's copy of it
+#pragma unroll
+      for (int m = 0; m < NCH / 2; ++m) {
+        const float send = b2 ? P[m] : P[m + NCH / 2];
+        const float keep = b2 ? P[m + NCH / 2] : P[m];
+        P[m] = keep + dpp_f<kDppHalfMirror>(send);
       }
 #pragma unroll
-      for (int m = 0; m < NOUT; ++m) {
-        float tot;
-        int row;  // row within this head's block_v rows
-        if constexpr (NBLK >= 4) {
-          const float send = hi2 ? R2[2 * m] : R2[2 * m + 1];
-          const float keep = hi2 ? R2[2 * m + 1] : R2[2 * m];
-          tot = keep + __shfl_xor(send, 32);
-          row = 64 * m + lane;
-        } else {
-          tot = R2[0] + __shfl_xor(R2[0], 32);
-          row = 16 * (q4 & 1) + l16;
+      for (int m = 0; m < NCH / 4; ++m) {
+        const float send = b1 ? P[m] : P[m + NCH / 4];
+        const float keep = b1 ? P[m + NCH / 4] : P[m];
+        P[m] = keep + dpp_f<kDppXor2>(send);
+      }
+      if constexpr (NCH >= 8) {
+#pragma unroll
+        for (int m = 0; m < NCH / 8; ++m) {
+          const float send = b0 ? P[m] : P[m + NCH / 8];
+          const float keep = b0 ? P[m + NCH / 8] : P[m];
+          P[m] = keep + dpp_f<kDppXor1>(send);
         }
-        // scale of the row's vblock: row >> 5 = 2 m + (lane >> 5) (NBLK >= 4), else 0
-        // (a bit-select: a plain select of the two entries is folded back into a
-        // lane-indexed load from a private array)
-        uint32_t sb = sc_bits[NBLK >= 4 ? 2 * m : 0];
-        if constexpr (NBLK >= 4) sb ^= (sb ^ sc_bits[2 * m + 1]) & (0u - (uint32_t)(lane >> 5));
-        const float sc = f16_bits_to_f32((uint16_t)sb);
-        if (NBLK >= 4 || q4 < 2) Act::st(out_rows, row, fmaf(tot, sc, wrow[m]) * a.out_scale);
+      } else {
+        P[0] += dpp_f<kDppXor1>(P[0]);
+      }
+      if (NCH >= 8 || b0 == 0) {
+#pragma unroll
+        for (int m = 0; m < NFIN; ++m) {
+          const int row = 8 * (ibase + m) + r8;
+          // scale of the row's vblock (row / 32 = (ibase + m) / 4), by bit-selects
+          // (a select of lane-indexed entries would become a private-array load)
+          const int pv = (ibase + m) >> 2;
+          uint32_t sb = sc_bits[0];
+#pragma unroll
+          for (int q = 1; q < NVB; ++q) sb ^= (sb ^ sc_bits[q]) & (0u - (uint32_t)(pv == q));
+          const float sc = f16_bits_to_f32((uint16_t)sb);
+          Act::st(out_rows, row, fmaf(P[m], sc, wrow[m]) * a.out_scale);
+        }
       }
       append_token();
       return;
