@@ -874,8 +874,9 @@ int gdnr_bf16_step(const gdnr_tensor* state, const gdnr_tensor* q, const gdnr_te
 
 int gdnr_bf16_step_packed(const gdnr_tensor* mixed_qkv, const gdnr_tensor* a, const gdnr_tensor* b,
                           const gdnr_tensor* a_log, const gdnr_tensor* dt_bias, const gdnr_tensor* state,
-                          const gdnr_tensor* state_indices, const gdnr_tensor* out, void* stream) {
+                          const gdnr_tensor* state_indices, const gdnr_tensor* out, float scale, void* stream) {
   g_last_error.clear();
+  if (!(scale - scale == 0.0f)) return fail(GDNR_ERR_INVALID_ARGUMENT, "scale: %g is not finite", (double)scale);
   GDNR_TRY(check_desc(state, "state", 4));
   GDNR_TRY(check_dtype(state, "state", {GDNR_DTYPE_BF16, GDNR_DTYPE_F16, GDNR_DTYPE_F32}));
   const int64_t S = state->shape[0], HV = state->shape[1], V = state->shape[2], K = state->shape[3];
@@ -929,7 +930,7 @@ int gdnr_bf16_step_packed(const gdnr_tensor* mixed_qkv, const gdnr_tensor* a, co
   r.out = out->data, r.o_b = out->strides[0], r.o_h = out->strides[2];
   r.B = (int32_t)B, r.HV = (int32_t)HV, r.V = (int32_t)V, r.G = (int32_t)(HV / H), r.H = (int32_t)H;
   r.n_slots = (int32_t)S;
-  r.out_scale = 1.0f / __builtin_sqrtf((float)K);
+  r.out_scale = scale;
   return hip_status(gdnr::launch_rmw_packed(r, state->dtype, act, a->dtype == GDNR_DTYPE_F32, stream));
 }
 

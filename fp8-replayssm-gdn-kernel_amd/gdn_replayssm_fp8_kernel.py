@@ -352,11 +352,13 @@ def gdn_bf16_step_packed(
     initial_state: torch.Tensor,
     ssm_state_indices: torch.Tensor,
     out: torch.Tensor | None = None,
+    scale: float | None = None,
 ) -> torch.Tensor:
     """The bf16 read-modify-write comparator in the production operator's
     contract (findings.md:35-45): q/k L2 norm and gating in the kernel,
     initial_state [slots, HV, V, K] updated in place at slot
-    ssm_state_indices[b] (slot 0 the null slot), out [B, 1, HV, V]."""
+    ssm_state_indices[b] (slot 0 the null slot), out [B, 1, HV, V] =
+    scale (S q); scale defaults to head_k_dim ** -0.5, as vLLM passes it."""
     device = _require_cuda(mixed_qkv=mixed_qkv, a=a, b=b, a_log=a_log, dt_bias=dt_bias,
                            initial_state=initial_state, ssm_state_indices=ssm_state_indices, out=out)
     batch = mixed_qkv.shape[0]
@@ -366,6 +368,7 @@ def gdn_bf16_step_packed(
     with torch.cuda.device(device):
         gdnr_lib.call("gdnr_bf16_step_packed", [mixed_qkv, a, b, a_log.float(), dt_bias.float(), initial_state,
                                                 _as_i32(ssm_state_indices), out], [],
-                      gdnr_lib.current_stream(device))
+                      gdnr_lib.current_stream(device),
+                      floats=[initial_state.shape[-1] ** -0.5 if scale is None else scale])
     return out
 

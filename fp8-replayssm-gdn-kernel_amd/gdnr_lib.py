@@ -56,7 +56,7 @@ class GdnrTensor(ctypes.Structure):
     ]
 
 
-# exported entry points: name -> number of gdnr_tensor* arguments, trailing int32 args
+# exported entry points: name -> number of gdnr_tensor* arguments, trailing int32 args[, trailing float args]
 ENTRY_POINTS = {
     "gdnr_replay_fp8": (10, 1),
     "gdnr_replay_fp8_split": (11, 3),
@@ -66,7 +66,7 @@ ENTRY_POINTS = {
     "gdnr_quantize_vblock32": (4, 0),
     "gdnr_dequantize_vblock32": (3, 0),
     "gdnr_bf16_step": (7, 0),
-    "gdnr_bf16_step_packed": (8, 0),
+    "gdnr_bf16_step_packed": (8, 0, 1),
     "gdnr_quantize_checkpoint": (4, 2),
     "gdnr_dequantize_checkpoint": (3, 2),
 }
@@ -88,10 +88,11 @@ def load_library(path: Path | None = None) -> ctypes.CDLL:
     lib.gdnr_last_error.argtypes = []
     lib.gdnr_abi_version.restype = ctypes.c_int
     lib.gdnr_abi_version.argtypes = []
-    for name, (n_tensors, n_ints) in ENTRY_POINTS.items():
+    for name, (n_tensors, n_ints, *n_floats) in ENTRY_POINTS.items():
         fn = getattr(lib, name)
         fn.restype = ctypes.c_int
-        fn.argtypes = [ctypes.POINTER(GdnrTensor)] * n_tensors + [ctypes.c_int32] * n_ints + [ctypes.c_void_p]
+        fn.argtypes = ([ctypes.POINTER(GdnrTensor)] * n_tensors + [ctypes.c_int32] * n_ints
+                       + [ctypes.c_float] * sum(n_floats) + [ctypes.c_void_p])
     if lib.gdnr_abi_version() != ABI_VERSION:
         raise RuntimeError(f"{path}: ABI version {lib.gdnr_abi_version()} != {ABI_VERSION}")
     if path == LIBRARY_PATH:
@@ -118,13 +119,13 @@ def describe(t: torch.Tensor | None) -> GdnrTensor | None:
     return desc
 
 
-def call(name: str, tensors, ints=(), stream: int | None = None) -> None:
+def call(name: str, tensors, ints=(), stream: int | None = None, floats=()) -> None:
     """Invoke an entry point; tensors must already be on the same CUDA device."""
     lib = load_library()
     fn = getattr(lib, name)
     descs = [describe(t) for t in tensors]
     ptrs = [ctypes.byref(d) if d is not None else None for d in descs]
-    status = fn(*ptrs, *[int(i) for i in ints], ctypes.c_void_p(stream))
+    status = fn(*ptrs, *[int(i) for i in ints], *[float(x) for x in floats], ctypes.c_void_p(stream))
     if status != 0:
         raise GdnrError(status, lib.gdnr_last_error().decode())
 

@@ -234,14 +234,16 @@ int gdnr_bf16_step(const gdnr_tensor* state, const gdnr_tensor* q, const gdnr_te
  * state_indices[b] (slot 0 the null slot; clamped on the device).
  * Shapes: mixed_qkv [B, 2*H*K + HV*V]; a, b [B,HV] (f32 or the mixed_qkv
  * dtype); a_log, dt_bias [HV] f32; state [S,HV,V,K] bf16|f16|f32;
- * state_indices [B] i32; out [B,1,HV,V] in the mixed_qkv dtype.
+ * state_indices [B] i32; out [B,1,HV,V] in the mixed_qkv dtype; scale
+ * multiplies o = S q (the production op's scale argument, head_k_dim^-1/2
+ * in vLLM's call; it must be finite).
  * The production op's contract is findings.md:35-45; the reference times its
  * full-contract step against it (prototype/bench_gdn_full_contract.py).
  */
 int gdnr_bf16_step_packed(const gdnr_tensor* mixed_qkv, const gdnr_tensor* a, const gdnr_tensor* b,
                           const gdnr_tensor* a_log, const gdnr_tensor* dt_bias,
                           const gdnr_tensor* state, const gdnr_tensor* state_indices,
-                          const gdnr_tensor* out, void* stream);
+                          const gdnr_tensor* out, float scale, void* stream);
 
 /*
  * Every checkpoint format of the reference's quantiser: granularity head,

@@ -278,14 +278,15 @@ def baseline_decode(initial_state, q, k, v, g, beta, dtype=np.float32):
     return np.concatenate(outputs, axis=1), state
 
 
-def bf16_rmw_step(state, q, k, v, g, beta, state_dtype="bf16", out_dtype="bf16", dtype=np.float32):
+def bf16_rmw_step(state, q, k, v, g, beta, state_dtype="bf16", out_dtype="bf16", dtype=np.float32, scale=None):
     """kernel:245-341 (host wrapper kernel:408-450): the full-state
     read-modify-write comparator. One token per sequence, in the kernel's
     order and fp32: S *= exp(g); r = sum_K(S k); c = (v - r) beta;
     S += c k^T; o = sum_K(S q) K^-1/2. S goes back in its storage dtype and
     o in the output dtype, both rounded to nearest even (round_to).
     state [B,HV,V,K]; q, k [B,H,K] (shared by the HV/H value heads of a key
-    head); v [B,HV,V]; g, beta [B,HV]. Returns (out, new_state) as float32
+    head); v [B,HV,V]; g, beta [B,HV]; scale (default K^-1/2) multiplies o.
+    Returns (out, new_state) as float32
     arrays holding values of those dtypes. Pinned (tests/test_oracle_rmw.py):
     with f32 storage it is run_kernel's one-token step (ref:155-161); from a
     zero state it is S = beta v k^T, o = beta v (k . q) K^-1/2; beta = 0 is
@@ -298,7 +299,7 @@ def bf16_rmw_step(state, q, k, v, g, beta, state_dtype="bf16", out_dtype="bf16",
     retrieved = (s * k_t[:, :, None, :]).sum(axis=-1)
     correction = (np.asarray(v, dtype=dtype) - retrieved) * np.asarray(beta, dtype=dtype)[..., None]
     s = s + correction[..., None] * k_t[:, :, None, :]
-    out = (s * q_t[:, :, None, :]).sum(axis=-1) * dtype(k.shape[-1] ** -0.5)
+    out = (s * q_t[:, :, None, :]).sum(axis=-1) * dtype(k.shape[-1] ** -0.5 if scale is None else scale)
     return round_to(out, out_dtype), round_to(s, state_dtype)
 
 
@@ -476,7 +477,8 @@ def prep_values(mixed_qkv, a, b, a_log, dt_bias, heads, key_dim, value_heads, va
     return q, k, v, g, beta
 
 
-def packed_rmw_step(state, slots, mixed_qkv, a, b, a_log, dt_bias, heads, state_dtype="bf16", out_dtype="bf16"):
+def packed_rmw_step(state, slots, mixed_qkv, a, b, a_log, dt_bias, heads, state_dtype="bf16", out_dtype="bf16",
+                    scale=None):
     """The comparator in the production operator's contract (findings.md:35-45):
     prep_values (q/k L2 norm, gates; kernel:504-562) then bf16_rmw_step on the
     state of slot slots[i] of state [S,HV,V,K]. Slots outside [0, S) read slot
@@ -494,7 +496,7 @@ def packed_rmw_step(state, slots, mixed_qkv, a, b, a_log, dt_bias, heads, state_
     idx = np.asarray(slots, dtype=np.int64)
     idx = np.where((idx >= 0) & (idx < state.shape[0]), idx, 0)
     out, new = bf16_rmw_step(state[idx], q.astype(np.float32), k.astype(np.float32), v.astype(np.float32),
-                             g.astype(np.float32), beta.astype(np.float32), state_dtype, out_dtype)
+                             g.astype(np.float32), beta.astype(np.float32), state_dtype, out_dtype, scale=scale)
     result = state.copy()
     live = idx != 0
     result[idx[live]] = new[live]

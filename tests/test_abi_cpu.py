@@ -264,9 +264,9 @@ def _packed_args(S=3, B=2, H=2, HV=4, K=128, V=128, act=BF16, gate=BF16, idx_dt=
             "state": desc([S, HV, V, K], BF16), "idx": desc([B], idx_dt), "out": desc([B, 1, HV, V], act)}
 
 
-def _packed_call(lib, args):
+def _packed_call(lib, args, scale=128 ** -0.5):
     order = ["mixed", "a", "b", "a_log", "dt_bias", "state", "idx", "out"]
-    rc = lib.gdnr_bf16_step_packed(*[ctypes.byref(args[n]) for n in order], None)
+    rc = lib.gdnr_bf16_step_packed(*[ctypes.byref(args[n]) for n in order], scale, None)
     return rc, lib.gdnr_last_error().decode()
 
 
@@ -286,6 +286,12 @@ def test_packed_step_rejects_misuse(lib, kwargs, change, code, needle):
     rc, msg = _packed_call(lib, args)
     assert rc == code, msg
     assert needle in msg, msg
+
+
+@pytest.mark.parametrize("scale", [float("nan"), float("inf")])
+def test_packed_step_rejects_a_non_finite_scale(lib, scale):
+    rc, msg = _packed_call(lib, _packed_args(), scale)
+    assert rc == INVALID and "scale" in msg, msg
 
 
 def test_packed_step_empty_batch_is_a_no_op(lib):

@@ -86,11 +86,11 @@ def test_rmw_step_two_tokens_in_place(device):
         assert rel_l2(np32(out), ref_out) <= 2e-3
 
 
-@pytest.mark.parametrize("state_dtype,act,gate", [(torch.bfloat16, torch.bfloat16, torch.bfloat16),
-                                                  (torch.bfloat16, torch.bfloat16, torch.float32),
-                                                  (torch.float32, torch.float16, torch.float16),
-                                                  (torch.float16, torch.float32, torch.float32)])
-def test_packed_step_matches_oracle(device, state_dtype, act, gate):
+@pytest.mark.parametrize("state_dtype,act,gate,scale", [(torch.bfloat16, torch.bfloat16, torch.bfloat16, None),
+                                                        (torch.bfloat16, torch.bfloat16, torch.float32, 0.05),
+                                                        (torch.float32, torch.float16, torch.float16, None),
+                                                        (torch.float16, torch.float32, torch.float32, None)])
+def test_packed_step_matches_oracle(device, state_dtype, act, gate, scale):
     """The production contract (gdnr_bf16_step_packed): 12 live sequences in
     out-of-order slots of a 20-slot state plus two padding entries (slot 0),
     raw mixed_qkv rows, q/k norm and gates in the kernel. Live slots follow
@@ -107,9 +107,10 @@ def test_packed_step_matches_oracle(device, state_dtype, act, gate):
     mixed, a, b = mixed[:, 0].contiguous(), a[:, 0].contiguous(), b[:, 0].contiguous()
     state = warm.clone()
     idx = torch.tensor(slots, dtype=torch.int32, device=device)
-    out = gk.gdn_bf16_step_packed(mixed, a, b, a_log, dt_bias, state, idx)
+    out = gk.gdn_bf16_step_packed(mixed, a, b, a_log, dt_bias, state, idx, scale=scale)
     ref_out, ref_state = gdn_oracle.packed_rmw_step(np32(warm), slots, np32(mixed), np32(a), np32(b), np32(a_log),
-                                                    np32(dt_bias), shape.heads, STORAGE[state_dtype], STORAGE[act])
+                                                    np32(dt_bias), shape.heads, STORAGE[state_dtype], STORAGE[act],
+                                                    scale=scale)
     assert out.shape == (len(slots), 1, shape.value_heads, shape.value_dim) and out.dtype == act
     live = [i for i, s in enumerate(slots) if s != 0]
     _check_state(state[live_slots], ref_state[live_slots], state_dtype)

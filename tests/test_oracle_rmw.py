@@ -147,3 +147,17 @@ def test_packed_permutation_and_null_slot():
     for sl in (0, 2, 3):
         assert np.array_equal(new[sl], state[sl])
     assert not np.array_equal(new[4], state[4]) and not np.array_equal(new[1], state[1])
+
+
+def test_packed_scale_only_scales_the_output():
+    """The production op's scale multiplies o and nothing else: a scale of
+    2 K^-1/2 gives exactly twice the output (a power of two) and the same
+    stored states."""
+    mixed, a, b, a_log, dt_bias = _packed_inputs(3)
+    rng = np.random.default_rng(6)
+    state = (0.1 * rng.standard_normal((S_SLOTS, HV, V, K))).astype(np.float32)
+    out1, new1 = gdn_oracle.packed_rmw_step(state, [1, 3], mixed, a, b, a_log, dt_bias, H, "f32", "f32")
+    out2, new2 = gdn_oracle.packed_rmw_step(state, [1, 3], mixed, a, b, a_log, dt_bias, H, "f32", "f32",
+                                            scale=2 * K ** -0.5)
+    assert np.array_equal(out2, 2 * out1)
+    assert np.array_equal(new2, new1)
