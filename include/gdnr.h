@@ -236,7 +236,9 @@ int gdnr_bf16_step(const gdnr_tensor* state, const gdnr_tensor* q, const gdnr_te
  * dtype); a_log, dt_bias [HV] f32; state [S,HV,V,K] bf16|f16|f32;
  * state_indices [B] i32; out [B,1,HV,V] in the mixed_qkv dtype; scale
  * multiplies o = S q (the production op's scale argument, head_k_dim^-1/2
- * in vLLM's call; it must be finite).
+ * in vLLM's call; it must be finite). A non-null slot may appear once per
+ * batch (entries sharing one race, as in the production op); padding
+ * entries all write the null slot, in an unspecified order.
  * The production op's contract is findings.md:35-45; the reference times its
  * full-contract step against it (prototype/bench_gdn_full_contract.py).
  */
