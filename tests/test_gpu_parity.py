@@ -295,3 +295,40 @@ def test_cycle_matches_oracle(device):
     got = np.stack(outs, axis=1)
     assert rel_l2(got, ref) <= OUT_TOL
     assert np.mean(codes_np(ck.payload) != ref_codes) < 1e-3
+
+
+@pytest.mark.parametrize("block_v", [32, 64, 128])
+def test_strided_views_equal_contiguous(device, block_v):
+    """Outer strides are free, as in the reference's wrappers: a checkpoint
+    whose rows sit 192 bytes apart (a view of a padded buffer), scales and
+    rings that are slices of larger buffers give bit-identical outputs and
+    requantised checkpoints to contiguous copies, and the padding is never
+    written. Fills 1..16 plus two flushes (L=16)."""
+    B, L = 8, 16
+    valid = [1, 4, 7, 9, 12, 15, 16, 16]
+    flush = [False] * 6 + [True, True]
+    case = make_replay_case(B, L, device, seed=21, valid=valid, flush=flush)
+    ck = case["ckpt"]
+    pad_payload = torch.full((B, 32, 128, 192), 0x55, dtype=torch.uint8, device=device)
+    pay_view = pad_payload[..., :128].view(torch.float8_e4m3fn)
+    pay_view.copy_(ck.payload)
+    pad_scale = torch.zeros(B, 32, 8, dtype=torch.float16, device=device)
+    sc_view = pad_scale[..., :4]
+    sc_view.copy_(ck.scale)
+
+    def ring_view(x):
+        big = torch.zeros(x.shape[0], 2 * L, *x.shape[2:], dtype=x.dtype, device=device)
+        big[:, :L].copy_(x)
+        return big[:, :L]
+
+    k, v, g, beta = (ring_view(case[n]) for n in ("k", "v", "g", "beta"))
+    out_view = gk.gdn_replay_fp8(pay_view, sc_view, case["q"], k, v, g, beta, case["valid"], case["flush"],
+                                 block_v=block_v)
+    payload_c, scale_c = ck.payload.clone(), ck.scale.clone()
+    out_c = gk.gdn_replay_fp8(payload_c, scale_c, case["q"], case["k"], case["v"], case["g"], case["beta"],
+                              case["valid"], case["flush"], block_v=block_v)
+    assert torch.equal(out_view, out_c)
+    assert torch.equal(pay_view.view(torch.uint8), payload_c.view(torch.uint8))
+    assert torch.equal(sc_view, scale_c)
+    assert bool((pad_payload[..., 128:] == 0x55).all())
+    assert bool((pad_scale[..., 4:] == 0).all())
