@@ -50,7 +50,7 @@ for _p in (REPO, PKG):
 
 METRIC = "µs per GDN-layer decode step (B=64, L=16) + achieved HBM GB/s % of peak"
 HBM_PEAK_GBS = 8000.0
-KERNEL_NAME = "step_kernel<ActBF16, 16, true, false>"
+KERNEL_NAME = "step_kernel<ActBF16, 16, true, {gate_f32}, false>"  # <act, NCH, fused, gate_f32, slots>
 CPU_SAMPLE_SECONDS = 10.0
 CPU_MAX_CYCLES = 8
 
@@ -74,6 +74,9 @@ def parse_args():
     p.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a HIP graph")
     p.add_argument("--no-rmw", action="store_true",
                    help="skip the same-box timing of the bf16 read-modify-write comparator")
+    p.add_argument("--trace", default=None,
+                   help="capture file (the production hook's record format) to take the decode inputs from")
+    p.add_argument("--trace-layer", type=int, default=0, help="layer of the capture file")
     p.add_argument("--no-mixed", action="store_true",
                    help="skip the same cycle timed again with staggered ring phases")
     p.add_argument("--no-slots", action="store_true",
@@ -171,10 +174,21 @@ def main() -> int:
     gen = synth.generator(0, device)
     a_log, dt_bias = synth.gating_params(shape, gen, device)
     t0 = time.perf_counter()
-    state = synth.warm_state(shape, 256, gen, device, a_log, dt_bias)
+    if args.trace:
+        # real decode inputs from a capture file (one layer's batch-1 record,
+        # replicated over the batch; its steps repeat when fewer than L)
+        import gdn_replayssm_capture as cap
+
+        inp = cap.captured_inputs(cap.load_capture(args.trace), B, args.trace_layer, L, device)
+        a_log, dt_bias = inp["a_log"], inp["dt_bias"]
+        reps = math.ceil(L / inp["mixed_qkv"].shape[1])
+        mixed, a_raw, b_raw = (inp[k].repeat(1, reps, 1)[:, :L].contiguous() for k in ("mixed_qkv", "a", "b"))
+        state = inp["state"]
+    else:
+        state = synth.warm_state(shape, 256, gen, device, a_log, dt_bias)
+        mixed, a_raw, b_raw = synth.raw_step_inputs(shape, L, gen, device)
     ck = gk.quantize_checkpoint(state, saturation=False)
     del state
-    mixed, a_raw, b_raw = synth.raw_step_inputs(shape, L, gen, device)
     mixed = [mixed[:, t].contiguous() for t in range(L)]
     a_raw = [a_raw[:, t].contiguous() for t in range(L)]
     b_raw = [b_raw[:, t].contiguous() for t in range(L)]
@@ -262,7 +276,8 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "f32",
         "storage": "fp8-e4m3fn checkpoint (fp16 vblock32 scales), bf16 ring/q/out",
-        "data": "synthetic (seeded; BASELINE distributions, 256-step warm-up state)",
+        "data": (f"capture {args.trace} layer {args.trace_layer} (batch-1 record replicated over the batch)"
+                 if args.trace else "synthetic (seeded; BASELINE distributions, 256-step warm-up state)"),
         "config": {
             "workload": (f"full-contract decode step (prep + replay, flush at l=L), one fused launch per step, "
                          f"Qwen3.5-4B GDN layer H=16 HV=32 K=V=128, B={B}, L={L}, cycle-amortised ({args.phase} "
@@ -274,7 +289,7 @@ def main() -> int:
         "algorithmic_bytes_per_step": bytes_step,
         "roofline": {
             "bound": "hbm",
-            "kernel": KERNEL_NAME,
+            "kernel": KERNEL_NAME.format(gate_f32="true" if a_raw[0].dtype == torch.float32 else "false"),
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",

@@ -165,3 +165,47 @@ def test_large_batch_stacked_layers(device, block_v):
     store[block_v] = digests
     for other, ref_digests in store.items():
         assert ref_digests == digests, f"block_v={block_v} differs from block_v={other}"
+
+
+def test_captured_inputs_drive_the_cycle(device, tmp_path):
+    """Real-trace mode (gdn_replayssm_capture, the capture format of
+    prototype/qwen35_capture_raw.py:100-130 as read by
+    bench_gdn_full_contract.py:83-110): a batch-1 record of one layer,
+    written and loaded back, replicated over 4 sequences, drives 10 steps of
+    the L=4 cycle. Every sequence gives the same outputs; they match the fp64
+    oracle of the cycle to rel-L2 <= 2e-3 and the record's production_out
+    (stored in bf16, so two bf16 roundings apart) to 3e-3."""
+    import gdn_replayssm_capture as cap
+
+    T, L, batch = 10, 4, 4
+    shape1 = synth.Shape(1)
+    gen = synth.generator(71, device)
+    a_log, dt_bias = synth.gating_params(shape1, gen, device)
+    state = synth.warm_state(shape1, 32, gen, device, a_log, dt_bias)
+    mixed, a, b = synth.raw_step_inputs(shape1, T, gen, device, gate_dtype=torch.float32)
+    ck1 = gk.quantize_checkpoint(state)
+    ref = gdn_oracle.full_contract_decode(codes_np(ck1.payload), ck1.scale.cpu().numpy(), np32(mixed), np32(a), np32(b),
+                                          np32(a_log), np32(dt_bias), L, shape1.heads, shape1.key_dim,
+                                          shape1.value_heads, shape1.value_dim, dtype=np.float64)[0][0]
+    record = {
+        "mixed_qkv": [mixed[:, t].cpu() for t in range(T)],
+        "a": [a[:, t].cpu() for t in range(T)],
+        "b": [b[:, t].cpu() for t in range(T)],
+        "production_out": [torch.from_numpy(ref[t].reshape(1, -1)).to(torch.bfloat16) for t in range(T)],
+        "state": state.cpu(),
+        "a_log": a_log.cpu(),
+        "dt_bias": dt_bias.cpu(),
+        "scale": shape1.key_dim ** -0.5,
+        "use_qk_l2norm_in_kernel": True,
+    }
+    path = tmp_path / "capture.pt"
+    cap.save_capture(path, {5: record})
+    inp = cap.captured_inputs(cap.load_capture(path), batch=batch, layer=5, steps=T, device=device)
+    ck = gk.quantize_checkpoint(inp["state"])
+    outs = _run_cycle(ck, inp["mixed_qkv"], inp["a"], inp["b"], inp["a_log"], inp["dt_bias"], L,
+                      np.zeros(batch, dtype=np.int64), T, 128, device)
+    prod = np32(inp["production_out"]).reshape(T, shape1.value_heads, shape1.value_dim)
+    for bi in range(batch):
+        assert np.array_equal(outs[bi], outs[0])
+    assert rel_l2(outs[0], ref) <= OUT_TOL
+    assert rel_l2(outs[0], prod) <= 3e-3
