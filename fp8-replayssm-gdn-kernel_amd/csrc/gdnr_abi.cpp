@@ -340,7 +340,7 @@ gdnr::StepArgs make_step_args(const gdnr::ReplayArgs& r, int es, int gate_es) {
   s.al_s = u32(4 * r.al_s), s.db_s = u32(4 * r.db_s);
   s.qo_b = u32(es * r.qo_b), s.qo_h = u32(es * r.qo_h);
   s.B = r.B, s.H = r.H, s.G = r.G, s.V = r.V, s.L = r.L, s.gw = r.gw, s.block_v = r.block_v, s.n_vt = r.n_vt;
-  s.sw = r.sw, s.rpw = r.rpw;
+  s.sw = r.sw, s.rpw = r.rpw, s.units = r.units;
   s.out_scale = r.out_scale;
   s.lds_q = r.lds_q, s.lds_knew = r.lds_knew, s.lds_k = r.lds_k, s.lds_flag = r.lds_flag, s.lds_c = r.lds_c;
   s.lds_t = r.lds_t, s.lds_g = r.lds_g, s.lds_v = r.lds_v, s.lds_r = r.lds_r, s.lds_fac = r.lds_fac;
@@ -427,13 +427,45 @@ void fill_index(const gdnr_tensor* t, const T** p, int64_t* s) {
   *s = t->strides[0];
 }
 
+// The decode kernel (gdnr_decode.hip) takes 16-bit activations, rings of up
+// to kStepRing tokens and V = 64, 128 or 256 (one wave of 64 or 128 rows per
+// value head, two of 128 rows for V = 256); gw value heads per workgroup
+// beside its chain wave. sw carries V / 64 to the launcher.
+bool decode_eligible(const gdnr::ReplayArgs& a, int act) {
+  return (act == GDNR_DTYPE_BF16 || act == GDNR_DTYPE_F16) && a.L <= gdnr::kStepRing &&
+         (a.V == 64 || a.V == 128 || a.V == 256);
+}
+void fit_decode(gdnr::ReplayArgs* a) {
+  const int32_t nwh = a->V == 256 ? 2 : 1;  // row waves per value head
+  a->gw = a->G % 2 == 0 ? 2 : 1;  // value heads per unit (at most 2; they share the unit's chain wave)
+  a->sw = a->V / 64;
+  // units per workgroup: as many as fit one CU (12 waves) while the grid
+  // still covers every CU, dividing the units of a sequence
+  const int32_t per_seq = a->H * (a->G / a->gw), waves = 1 + a->gw * nwh;
+  a->units = 1;
+  for (int32_t u : {4, 2}) {
+    if (per_seq % u == 0 && u * waves <= 12 && (int64_t)a->B * per_seq / u >= gdnr::device_cus()) {
+      a->units = u;
+      break;
+    }
+  }
+  a->lds_bytes = gdnr::decode_lds_bytes(a->units, a->gw * nwh, a->V == 64 ? 2 : 4);
+}
+int launch_decode(const gdnr::ReplayArgs& r, int act, bool fused, bool gate_f32, void* stream) {
+  gdnr::StepArgs a = make_step_args(r, elem_size(act), gate_f32 ? 4 : elem_size(act));
+  a.status = gdnr::status_word();
+  if (act == GDNR_DTYPE_BF16) return gdnr::launch_decode_bf16(a, fused, gate_f32, stream);
+  return gdnr::launch_decode_f16(a, fused, gate_f32, stream);
+}
+
 int launch_replay(const gdnr::ReplayArgs& a, int act, int mode, bool gate_f32, void* stream) {
   if (act == GDNR_DTYPE_BF16) return gdnr::launch_replay_bf16(a, mode, gate_f32, stream);
   if (act == GDNR_DTYPE_F16) return gdnr::launch_replay_f16(a, mode, gate_f32, stream);
   return gdnr::launch_replay_f32(a, mode, gate_f32, stream);
 }
 int launch_step(const gdnr::ReplayArgs& r, int act, bool fused, bool gate_f32, void* stream) {
-  const gdnr::StepArgs a = make_step_args(r, elem_size(act), gate_f32 ? 4 : elem_size(act));
+  gdnr::StepArgs a = make_step_args(r, elem_size(act), gate_f32 ? 4 : elem_size(act));
+  a.status = gdnr::status_word();
   if (act == GDNR_DTYPE_BF16) return gdnr::launch_step_bf16(a, fused, gate_f32, stream);
   if (act == GDNR_DTYPE_F16) return gdnr::launch_step_f16(a, fused, gate_f32, stream);
   return gdnr::launch_step_f32(a, fused, gate_f32, stream);
@@ -555,6 +587,14 @@ const char* gdnr_last_error(void) { return g_last_error.c_str(); }
 
 int gdnr_abi_version(void) { return GDNR_ABI_VERSION; }
 
+int gdnr_wait_timeouts(uint32_t* count, int32_t reset) {
+  g_last_error.clear();
+  if (!count) return fail(GDNR_ERR_INVALID_ARGUMENT, "count is NULL");
+  const int rc = gdnr::read_status(count, reset != 0);
+  if (rc) return fail(GDNR_ERR_HIP, "reading the wait status word failed: %s", gdnr::hip_error_string(rc));
+  return GDNR_OK;
+}
+
 int gdnr_replay_fp8(const gdnr_tensor* checkpoint, const gdnr_tensor* checkpoint_scale, const gdnr_tensor* q,
                     const gdnr_tensor* k_cache, const gdnr_tensor* v_cache, const gdnr_tensor* g_cache,
                     const gdnr_tensor* beta_cache, const gdnr_tensor* valid_len, const gdnr_tensor* flush,
@@ -582,6 +622,10 @@ int gdnr_replay_fp8(const gdnr_tensor* checkpoint, const gdnr_tensor* checkpoint
   a.o_b = out->strides[0];
   a.o_h = out->strides[1];
   if (a.L <= gdnr::kStepRing && step_offsets_fit(a, elem_size(g.act))) {
+    if (decode_eligible(a, g.act)) {
+      fit_decode(&a);
+      return hip_status(launch_decode(a, g.act, false, false, stream));
+    }
     GDNR_TRY(fit_step(&a, elem_size(g.act)));
     return hip_status(launch_step(a, g.act, false, false, stream));
   }
@@ -740,6 +784,10 @@ int gdnr_prep_replay_fp8(const gdnr_tensor* mixed_qkv, const gdnr_tensor* a, con
   r.o_b = out->strides[0];
   r.o_h = out->strides[1];
   if (r.L <= gdnr::kStepRing && step_offsets_fit(r, elem_size(g.act))) {
+    if (decode_eligible(r, g.act)) {
+      fit_decode(&r);
+      return hip_status(launch_decode(r, g.act, true, a->dtype == GDNR_DTYPE_F32, stream));
+    }
     GDNR_TRY(fit_step(&r, elem_size(g.act)));
     return hip_status(launch_step(r, g.act, true, a->dtype == GDNR_DTYPE_F32, stream));
   }
@@ -791,6 +839,10 @@ int gdnr_prep_replay_fp8_slots(const gdnr_tensor* mixed_qkv, const gdnr_tensor* 
   r.o_h = out->strides[1];
   if (!step_offsets_fit(r, elem_size(g.act)))
     return fail(GDNR_ERR_UNSUPPORTED, "state_indices: the slot tensors must span less than 2 GiB each");
+  if (decode_eligible(r, g.act)) {
+    fit_decode(&r);
+    return hip_status(launch_decode(r, g.act, true, a->dtype == GDNR_DTYPE_F32, stream));
+  }
   GDNR_TRY(fit_step(&r, elem_size(g.act)));
   return hip_status(launch_step(r, g.act, true, a->dtype == GDNR_DTYPE_F32, stream));
 }

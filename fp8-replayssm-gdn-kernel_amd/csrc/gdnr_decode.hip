@@ -1,0 +1,862 @@
+// gdnr_decode.hip -- the ReplaySSM decode step on gfx950 (MI355X) for rings of
+// up to 16 tokens with 16-bit activations (bf16 or f16): replay or flush per
+// sequence, optionally fused with the full-contract preparation of the new
+// token. (f32 activations take the step kernel of gdnr_step.hip.)
+//
+// The checkpoint stream starts at the first instruction of every wave. The
+// coefficient chain of a head does not stand between the stream and the
+// output: every wave projects its checkpoint rows on all ring keys and the
+// query with bf16/f16 MFMAs,
+//   P = X S_0^T,   X = [k_0 .. k_{n-1}, q, 0 ..]   (16 x 128, tokens x K),
+// and the chain only supplies the weights that combine those projections.
+// Replay, the adjoint of the reference's reverse chain
+// (prototype/gdn_replayssm_fp8_kernel.py:121-173) in Gram form:
+//   s_t = beta_t (dq_t - sum_{u>t} G_tu s_u),  G = K K^T,  dq = K q
+//   c_t = s_t prod_{u>t} gamma_u,  lam = prod_u gamma_u
+//   o   = (scale (lam P_q - sum_t lam s_t P_t) + sum_t c_t v_t) K^-1/2
+// (scale * codes is the dequantised checkpoint, so S_0 T_0 with the
+// reference's T_0 = lam (q - sum_t s_t k_t) is sum_t alpha_t P_t.)
+// Flush, the forward rebuild of kernel:177-242 in matrix form (W = V - pre P,
+// U = (I + M)^-1 W, S_n = lam S_0 + K^T (post U)), o from the rebuilt state,
+// requantisation in place with the reference quantiser (ref:36-37,83-99).
+//
+// Grid: x = group of gw value heads within the key head, y = key head h,
+// z = sequence b. Workgroup: gw value heads x nwh waves, wave (j, part)
+// owning V-rows [64 part, +64) of value head j. One wave per head (the
+// chain wave, part == (b + h) % nwh) also forms the head's Gram matrix and
+// coefficient chain (or flush factors) and publishes them through LDS; the
+// others wait for its flag only after their own projections are done.
+//
+// Operand layouts (16x16x32 MFMA; lane = 16 q4 + l16):
+//   X (A operand): lane (t = l16, q4) holds X[t][kappa(m, q4) + 0..7] for
+//     k-step m = 0..3, kappa(m, q4) = 64 (m >> 1) + 16 q4 + 8 (m & 1): the
+//     32 bytes at 32 q4 and at 128 + 32 q4 of the row.
+//   codes (B operand) of tile i (16 rows): lane (nn = l16, q4) holds row
+//     r(i, nn) = 32 (i >> 1) + 2 nn + (i & 1) of the wave's rows, bytes
+//     [16 q4, +16) and [64 + 16 q4, +16). Tiles 2p, 2p + 1 are vblock p of
+//     the wave, and a lane's rows of a token's v sit in two 4-byte pairs.
+//   P (accumulator): lane (nn, q4) holds P[token 4 q4 + e][row r(i, nn)].
+//
+// Compiled once per 16-bit activation dtype (GDNR_ACT = 0 bf16, 1 f16).
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <type_traits>
+
+#include "gdnr_device.h"
+#include "gdnr_internal.h"
+
+#ifndef GDNR_ACT
+#error "compile with -DGDNR_ACT=0|1|2"
+#endif
+
+#if GDNR_ACT != 2
+
+namespace gdnr {
+namespace {
+
+constexpr int K = kKeyDim;
+constexpr int NT = kStepRing;  // token rows of the operands (ring capacity <= 16)
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+#if GDNR_ACT == 0
+using Act = ActBF16;
+#define GDNR_SUFFIX(name) name##_bf16
+#else
+using Act = ActF16;
+#define GDNR_SUFFIX(name) name##_f16
+#endif
+constexpr bool kBF16 = std::is_same<Act, ActBF16>::value;
+
+__device__ __forceinline__ f32x4_t mfma16(u32x4_t a, u32x4_t b, f32x4_t c) {
+  if constexpr (kBF16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c,
+                                                   0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c,
+                                                  0, 0, 0);
+}
+// 4 e4m3 codes -> 4 values of the activation type (exact), packed in pairs
+__device__ __forceinline__ uint2 codes4(uint32_t w) { return kBF16 ? fp8x4_to_bf16x4(w) : fp8x4_to_f16x4(w); }
+// the 8 codes of k-step m of a row's 32 bytes (c[0]: bytes at 16 q4, c[1]: at 64 + 16 q4)
+__device__ __forceinline__ u32x4_t codes8(const u32x4_t* c, int m) {
+  const u32x4_t w = c[m >> 1];
+  const uint32_t w0 = (m & 1) ? w[2] : w[0], w1 = (m & 1) ? w[3] : w[1];
+  const uint2 lo = codes4(w0);
+  const uint2 hi = codes4(w1);
+  return u32x4_t{lo.x, lo.y, hi.x, hi.y};
+}
+// activation value from 16 bits
+__device__ __forceinline__ float act_val(uint32_t bits16) { return Act::from_bits(bits16 & 0xFFFFu); }
+__device__ __forceinline__ uint32_t act_bits(float x) {
+  if constexpr (kBF16) return f32_to_bf16(x);
+  else return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x);
+}
+
+__device__ __forceinline__ float rdl(float x, int lane) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), lane));
+}
+__device__ __forceinline__ int uni(int x) { return __builtin_amdgcn_readfirstlane(x); }
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t h) { return (float)__builtin_bit_cast(_Float16, (uint16_t)h); }
+
+// uniform loads through the scalar cache of data this kernel does not write
+// before reading it (constant address space; they count in lgkmcnt)
+typedef __attribute__((address_space(4))) const uint32_t const_u32;
+__device__ __forceinline__ uint32_t ld_u32_uniform(const void* p) { return *(const_u32*)p; }
+__device__ __forceinline__ uint32_t ld_u16_uniform(const uint8_t* p) {
+  const uintptr_t ad = (uintptr_t)p;
+  return (ld_u32_uniform((const void*)(ad & ~(uintptr_t)3)) >> (8u * (uint32_t)(ad & 2))) & 0xFFFFu;
+}
+__device__ __forceinline__ u32x4_t ld16(const uint8_t* p) { return *(const u32x4_t*)p; }
+// A wave-uniform pointer the compiler cannot see through: loads from it are
+// neither merged with nor hoisted above earlier loads of the same rows.
+__device__ __forceinline__ uint8_t* opaque_uniform(uint8_t* p) {
+  const uint64_t v = (uint64_t)p;
+  uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+  uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(v >> 32));
+  asm volatile("" : "+s"(lo), "+s"(hi));
+  return (uint8_t*)(((uint64_t)hi << 32) | lo);
+}
+typedef __attribute__((address_space(1))) const u32x4_t g_u32x4;
+typedef __attribute__((address_space(1))) u32x4_t g_u32x4_w;
+__device__ __forceinline__ uint32_t ld32(const uint8_t* p) { return *(const uint32_t*)p; }
+
+// DPP move within a 16-lane row; lanes whose source is outside the row get `fill`
+template <int CTRL>
+__device__ __forceinline__ float dpp_row(float x, float fill) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, fill), __builtin_bit_cast(int, x),
+                                                               CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float row_prefix_prod(float x) {
+  x *= dpp_row<0x111>(x, 1.f);
+  x *= dpp_row<0x112>(x, 1.f);
+  x *= dpp_row<0x114>(x, 1.f);
+  x *= dpp_row<0x118>(x, 1.f);
+  return x;
+}
+__device__ __forceinline__ float row_suffix_prod(float x) {
+  x *= dpp_row<0x101>(x, 1.f);
+  x *= dpp_row<0x102>(x, 1.f);
+  x *= dpp_row<0x104>(x, 1.f);
+  x *= dpp_row<0x108>(x, 1.f);
+  return x;
+}
+
+// Sum over the four 16-lane rows of per-tile partials: p[i] is lane (nn, q4)'s
+// partial of tile i; on return lane (nn, q4) holds the total of tile q4
+// (v_permlane32_swap then v_permlane16_swap: a reduce-scatter in 3 swaps).
+__device__ __forceinline__ float rows_reduce_scatter(float p0, float p1, float p2, float p3) {
+  const auto r0 = __builtin_amdgcn_permlane32_swap(__float_as_uint(p0), __float_as_uint(p2), false, false);
+  const auto r1 = __builtin_amdgcn_permlane32_swap(__float_as_uint(p1), __float_as_uint(p3), false, false);
+  const float u0 = __uint_as_float(r0[0]) + __uint_as_float(r0[1]);
+  const float u1 = __uint_as_float(r1[0]) + __uint_as_float(r1[1]);
+  const auto r2 = __builtin_amdgcn_permlane16_swap(__float_as_uint(u0), __float_as_uint(u1), false, false);
+  return __uint_as_float(r2[0]) + __uint_as_float(r2[1]);
+}
+
+extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+
+// LDS of a workgroup (bytes). The chain wave writes everything before the
+// workgroup barrier; the row waves only read it after.
+constexpr int kXStride = 272;                  // X row stride (256 + 16: conflict-free operand reads)
+constexpr int kLX = 0;                         // X rows [16][kXStride], the A operand in row form
+constexpr int kLQK = kLX + 16 * kXStride;      // the prepared q and k rows [2][256] (pair layout = row form)
+constexpr int kLKT = kLQK + 512;               // K^T operand tiles [8][16][16] act (flush)
+constexpr int kLG = kLKT + 8 * 16 * 16 * 2;    // Gram rows f32 [16][16]
+constexpr int kLDq = kLG + 1024;               // k_t . q of a full ring f32 [16]
+constexpr int kLHeads = kLDq + 64;             // per value head blocks
+// per value head (offsets from the head's block)
+constexpr int kHCoef = 0;                      // f32 [16]: c_t (replay)
+constexpr int kHLam = kHCoef + 64;             // f32 [4]: lam, the scale of the T_0 rows
+constexpr int kHFac = kHLam + 16;              // float4 [16]: (pre, post, dq, 0) (flush)
+constexpr int kHT0 = kHFac + 256;              // act [3][128]: T_0 as hi, mid and lo rows (replay)
+constexpr int kHR = kHT0 + 768;                // f32 [16][16]: R = (I + M)^-1 (flush)
+constexpr int kHM = kHR + 1024;                // f32 [16][16]: M (chain scratch)
+constexpr int kHeadLds = kHM + 1024;
+constexpr int kMaxDecodeHeads = 2;            // value heads per unit (gw)
+constexpr int kUnitBase = kLHeads + kMaxDecodeHeads * kHeadLds;  // LDS of one unit before its v rows
+// then (flush) the v rows of each of its row waves: lane l's 16 VB bytes at 16 VB l
+__host__ __device__ constexpr int unit_lds(int rpu, int vb) { return kUnitBase + rpu * 64 * 16 * vb; }
+
+// raw bits of a gating input (f32, or the activation dtype) and their value
+template <bool GATE_F32>
+__device__ __forceinline__ uint32_t gate_bits(const uint8_t* p) {
+  if constexpr (GATE_F32) return ld32(p);
+  else return *(const uint16_t*)p;
+}
+template <bool GATE_F32>
+__device__ __forceinline__ float gate_value(uint32_t bits) {
+  if constexpr (GATE_F32) return __uint_as_float(bits);
+  else return act_val(bits);
+}
+
+// Workgroup roles: wave 0 is the chain wave of the workgroup's key head (it
+// streams no checkpoint rows: a wave whose loads back up in the memory
+// pipeline cannot issue anything else, and the chain would wait behind
+// them); waves 1 + NWH j + part own V-rows [64 part, +64) of value head j.
+// The first kernel arguments (the key ring and checkpoint addressing, the
+// ring length and the head grouping) are preloaded into SGPRs at wave launch
+// (gfx950 kernarg preload, the build's -amdgpu-kernarg-preload-count): the
+// first requests of every wave issue before any scalar load returns.
+// Everything else comes from the StepArgs block.
+template <int TPW, int NWH, bool FUSED, bool GATE_F32, bool SLOTS>
+__global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void decode_kernel(
+    uint8_t* ckpt, uint8_t* kring, uint32_t ck_b, uint32_t ck_h, uint32_t ck_v, uint32_t k_b, uint32_t k_t,
+    uint32_t k_h, int32_t L, int32_t G, int32_t shape, const StepArgs a) {
+  constexpr int ES = 2;
+  const int lane = threadIdx.x & 63;
+  const int q4 = lane >> 4, l16 = lane & 15;
+  const int w = uni(threadIdx.x >> 6);
+  const int gw = shape & 0xFF, U = shape >> 8;  // value heads per unit, units per workgroup
+  const int rpu = gw * NWH;                     // row waves per unit
+  const bool chain = w < U;                     // waves [0, U): the chain waves
+  // (uniform indices: the divisions are VALU code, readfirstlane keeps the
+  // results and every address built from them in SGPRs)
+  const int u = uni(chain ? w : (w - U) / rpu);  // the wave's unit
+  const int r = (int)blockIdx.x * U + u;         // unit within the sequence: (key head, group)
+  const int n_grp = uni(G / gw);
+  const int h = uni(r / n_grp), grp = r - h * n_grp, b = blockIdx.y;
+  const int hv0 = h * G + grp * gw;              // first value head of the unit
+  uint8_t* const ul = lds + u * unit_lds(rpu, TPW / 2);  // the unit's LDS block
+
+  int bs = b;
+  if constexpr (SLOTS) {
+    const int sl = (int)uni((int)ld_u32_uniform(a.slot + b * a.sl_s));
+    bs = (sl >= 0 && sl < a.n_slots) ? sl : 0;
+  }
+  // per-sequence metadata (scalar; needed by every wave)
+  auto read_meta = [&](int& n, int& pos, bool& do_flush) {
+    const int n_raw = (int)ld_u32_uniform(a.valid_len + b * a.vl_s);
+    int pos_raw = -1;
+    if constexpr (FUSED) pos_raw = (int)ld_u32_uniform(a.pos + b * a.pos_s);
+    uint32_t flush_word = 0, flush_shift = 0;
+    if (a.flush) {
+      const uintptr_t fa = (uintptr_t)(a.flush + b * a.fl_s);
+      flush_word = ld_u32_uniform((const void*)(fa & ~(uintptr_t)3));
+      flush_shift = 8u * (uint32_t)(fa & 3);
+    }
+    n = min(max(uni(n_raw), 0), L);
+    pos = -1;
+    if constexpr (FUSED) {
+      const int p = uni(pos_raw);
+      pos = (p >= 0 && p < L) ? p : -1;
+    }
+    do_flush = uni((int)((flush_word >> flush_shift) & 0xFFu)) != 0;
+  };
+
+  if (chain) {
+    // ================= chain wave =================================================
+    // ---- loads: the key ring in the X layout (all 16 rows; rows at or past
+    // the fill are zeroed below), the query / new-token rows, the gates of
+    // every value head of the workgroup (lane t: token t)
+    const int tl = l16 < L ? l16 : 0;
+    const uint8_t* krow = kring + (bs * k_b + h * k_h + (uint32_t)tl * k_t) + 32 * q4;
+    u32x4_t xr[4];
+    xr[0] = ld16(krow);
+    xr[1] = ld16(krow + 16);
+    xr[2] = ld16(krow + 128);
+    xr[3] = ld16(krow + 144);
+    GDNR_COMPILER_FENCE();
+    uint32_t qbits, kbits = 0;
+    if constexpr (FUSED) {
+      const uint8_t* row = a.mixed + b * a.mx_b;
+      qbits = ld32(row + (h * K + 2 * lane) * ES);
+      kbits = ld32(row + (a.H * K + h * K + 2 * lane) * ES);
+    } else {
+      qbits = ld32(a.q + (b * a.q_b + h * a.q_h) + 4 * lane);
+    }
+    // the gates of the (at most kMaxDecodeHeads) value heads, lane t: token t
+    const int tl2 = l16 < L ? l16 : 0;
+    uint32_t g_raw[kMaxDecodeHeads], be_raw[kMaxDecodeHeads], ab_raw[kMaxDecodeHeads][2];
+    float alog[kMaxDecodeHeads], dtb[kMaxDecodeHeads];
+#pragma unroll
+    for (int j = 0; j < kMaxDecodeHeads; ++j) {
+      const int hv = hv0 + (j < gw ? j : 0);
+      g_raw[j] = *(const uint16_t*)(a.g + (bs * a.g_b + (uint32_t)tl2 * a.g_t + hv * a.g_h));
+      be_raw[j] = *(const uint16_t*)(a.beta + (bs * a.be_b + (uint32_t)tl2 * a.be_t + hv * a.be_h));
+      if constexpr (FUSED) {
+        ab_raw[j][0] = gate_bits<GATE_F32>(a.a + (b * a.a_b + hv * a.a_h));
+        ab_raw[j][1] = gate_bits<GATE_F32>(a.bgate + (b * a.bg_b + hv * a.bg_h));
+        alog[j] = *(const float*)(a.a_log + hv * a.al_s);
+        dtb[j] = *(const float*)(a.dt_bias + hv * a.db_s);
+      }
+    }
+    // (barrier 1: the chain requests of the workgroup enter the memory
+    // pipeline before any checkpoint row; the row waves wait here)
+    GDNR_COMPILER_FENCE();
+    __builtin_amdgcn_s_barrier();
+    GDNR_COMPILER_FENCE();
+    int n, pos;
+    bool do_flush;
+    read_meta(n, pos, do_flush);
+    const bool full = n >= NT;
+    // every load above is needed next; waiting for them here keeps later
+    // waits from covering the ring-append stores
+    GDNR_WAIT_VMCNT(0);
+
+    // ---- the query (and new key) rows: normalised as the preparation does
+    // (x / sqrt(sum x^2 + 1e-6), lane pairs, rounded to the ring dtype); the
+    // pair layout is the row form: element c at byte 2 c
+    {
+      const float2 qr = Act::from_pair(qbits);
+      uint32_t qw, kw = 0;
+      if constexpr (FUSED) {
+        const float2 kr = Act::from_pair(kbits);
+        const float qd = sqrtf(wave_sum(fmaf(qr.y, qr.y, qr.x * qr.x)) + 1e-6f);
+        const float kd = sqrtf(wave_sum(fmaf(kr.y, kr.y, kr.x * kr.x)) + 1e-6f);
+        qw = act_bits(Act::round(qr.x / qd)) | (act_bits(Act::round(qr.y / qd)) << 16);
+        kw = act_bits(Act::round(kr.x / kd)) | (act_bits(Act::round(kr.y / kd)) << 16);
+        // q_out and the ring append of the new key (one unit per key head)
+        if (grp == 0) {
+          *(uint32_t*)(a.q_out + (b * a.qo_b + h * a.qo_h) + 4 * lane) = qw;
+          if (pos >= 0) *(uint32_t*)(kring + (bs * k_b + (uint32_t)pos * k_t + h * k_h) + 4 * lane) = kw;
+        }
+      } else {
+        qw = qbits;
+      }
+      *(uint32_t*)(ul + kLQK + 4 * lane) = qw;
+      *(uint32_t*)(ul + kLQK + 256 + 4 * lane) = kw;
+    }
+    // ---- X rows: t < n the ring (the new token's own row at t == pos), t == n
+    // the query, the rest zero (a full ring, n == 16, takes the query as a
+    // block of its own: the q row of kLQK); written to LDS in row form
+    u32x4_t xa[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const int off = 128 * (m >> 1) + 16 * (m & 1) + 32 * q4;
+      const u32x4_t z = {0u, 0u, 0u, 0u};
+      const u32x4_t qv = *(const u32x4_t*)(ul + kLQK + off);
+      u32x4_t x = l16 < n ? xr[m] : (l16 == n ? qv : z);
+      if constexpr (FUSED) {
+        const u32x4_t kv = *(const u32x4_t*)(ul + kLQK + 256 + off);
+        x = (l16 == pos && l16 < n) ? kv : x;
+      }
+      xa[m] = x;
+      *(u32x4_t*)(ul + kLX + l16 * kXStride + off) = x;
+    }
+    // ---- Gram matrix G = X X^T (rows t < n; the query row n gives k_t . q)
+    f32x4_t gacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int m = 0; m < 4; ++m) gacc = mfma16(xa[m], xa[m], gacc);
+    float* Gs = (float*)(ul + kLG);
+    float* Dq = (float*)(ul + kLDq);
+    // G[4 q4 + e][u] at lane (u, q4) is row u, columns 4 q4 + e (symmetric)
+    *(float4*)(Gs + l16 * 16 + 4 * q4) = make_float4(gacc[0], gacc[1], gacc[2], gacc[3]);
+    if (full) {
+      f32x4_t dacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const int off = 128 * (m >> 1) + 16 * (m & 1) + 32 * q4;
+        const u32x4_t qv = *(const u32x4_t*)(ul + kLQK + off);
+        dacc = mfma16(xa[m], l16 == 0 ? qv : u32x4_t{0u, 0u, 0u, 0u}, dacc);
+      }
+      if (l16 == 0) *(float4*)(Dq + 4 * q4) = make_float4(dacc[0], dacc[1], dacc[2], dacc[3]);
+    }
+    const bool on = l16 < n;
+    float gcol[NT];  // G[lane token][t], zero for t >= n
+    {
+      const float4* gr = (const float4*)(Gs + l16 * 16);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float4 v4 = gr[i];
+        gcol[4 * i] = v4.x, gcol[4 * i + 1] = v4.y, gcol[4 * i + 2] = v4.z, gcol[4 * i + 3] = v4.w;
+      }
+#pragma unroll
+      for (int t = 0; t < NT; ++t) gcol[t] = t < n ? gcol[t] : 0.f;
+    }
+    const float dq = on ? (full ? Dq[l16] : Gs[l16 * 16 + (full ? 0 : n)]) : 0.f;
+    if (do_flush) {
+      // K^T operand tiles [ct][M][token] (flush): element (t, col) of X with
+      // col = kappa(m, q4) + j8 goes to tile ct = 2 m + j8 / 4, row
+      // M = 4 q4 + j8 % 4; tokens t >= n are zero
+      uint16_t* kt = (uint16_t*)(ul + kLKT);
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const u32x4_t x = on ? xa[m] : u32x4_t{0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int j8 = 0; j8 < 8; ++j8) {
+          const uint16_t e16 = (uint16_t)((x[j8 >> 1] >> (16 * (j8 & 1))) & 0xFFFFu);
+          kt[((2 * m + (j8 >> 2)) * 16 + 4 * q4 + (j8 & 3)) * 16 + l16] = e16;
+        }
+      }
+    }
+
+    // ---- per value head: gates, then the coefficient chain or the flush factors
+#pragma unroll
+    for (int j = 0; j < kMaxDecodeHeads; ++j) {
+      if (j >= gw) break;
+      const int hv = hv0 + j;
+      uint8_t* hl = ul + kLHeads + j * kHeadLds;
+      float gg = act_val(g_raw[j]);
+      float bb = act_val(be_raw[j]);
+      if constexpr (FUSED) {
+        // the new token's gates from the preparation formulas (kernel:534-562)
+        const float a_in = gate_value<GATE_F32>(ab_raw[j][0]), b_in = gate_value<GATE_F32>(ab_raw[j][1]);
+        const float x = a_in + dtb[j];
+        const float sp = x <= 20.0f ? logf(1.0f + expf(x)) : x;  // kernel:560, as written there
+        const float gate_new = Act::round(-expf(alog[j]) * sp);
+        const float beta_new = Act::round(1.0f / (1.0f + expf(-b_in)));
+        if (pos >= 0 && lane == 0) {
+          *(uint16_t*)(a.g + (bs * a.g_b + (uint32_t)pos * a.g_t + hv * a.g_h)) = (uint16_t)act_bits(gate_new);
+          *(uint16_t*)(a.beta + (bs * a.be_b + (uint32_t)pos * a.be_t + hv * a.be_h)) = (uint16_t)act_bits(beta_new);
+        }
+        gg = l16 == pos ? gate_new : gg;
+        bb = l16 == pos ? beta_new : bb;
+      }
+      const float gam = on ? expf(gg) : 1.f;
+      const float bet = on ? bb : 0.f;
+      const float suf_in = row_suffix_prod(gam);
+      const float suf_ex = dpp_row<0x101>(suf_in, 1.f);
+      const float lam = rdl(suf_in, 0);
+      if (lane == 0) ((float*)(hl + kHLam))[0] = lam;
+      if (!do_flush) {
+        // s_t, t descending: acc_l = sum_{u > t} G[l][u] s_u
+        float acc = 0.f, s_mine = 0.f;
+#pragma unroll
+        for (int t = NT - 1; t >= 0; --t) {
+          const float sv = rdl(bet * (dq - acc), t);
+          s_mine = l16 == t ? sv : s_mine;
+          acc = fmaf(gcol[t], sv, acc);
+        }
+        const float c = on ? s_mine * suf_ex : 0.f;
+        const float al = on ? -lam * s_mine : (l16 == n ? lam : 0.f);
+        if (lane < NT) ((float*)(hl + kHCoef))[lane] = c;
+        // T_0 = sum_t alpha_t X_t (+ lam q for a full ring) = lam (q - sum_t s_t k_t),
+        // the reference's transformed query; lane c2 holds columns 2 c2, 2 c2 + 1
+        float tx = 0.f, ty = 0.f;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          const float at = rdl(al, t);
+          const float2 xv = Act::from_pair(*(const uint32_t*)(ul + kLX + t * kXStride + 4 * lane));
+          tx = fmaf(at, xv.x, tx);
+          ty = fmaf(at, xv.y, ty);
+        }
+        if (full) {
+          const float2 qv = Act::from_pair(*(const uint32_t*)(ul + kLQK + 4 * lane));
+          tx = fmaf(lam, qv.x, tx);
+          ty = fmaf(lam, qv.y, ty);
+        }
+        // the MFMA operand: T_0 = hi + mid + lo, three 16-bit rows (the f32
+        // value to its last bits); f16 rows are scaled by a power of two
+        // first so that the smaller parts keep their precision
+        float t0s = 1.f;
+        if constexpr (!kBF16) {
+          const float mx =
+              __uint_as_float(wave_max_u32(max(__float_as_uint(fabsf(tx)), __float_as_uint(fabsf(ty)))));
+          if (mx > 0.f && mx < __builtin_inff()) {
+            int ex;
+            (void)frexpf(mx, &ex);
+            ex = uni(ex);
+            tx = ldexpf(tx, -ex);
+            ty = ldexpf(ty, -ex);
+            t0s = ldexpf(1.f, ex);
+          }
+        }
+        const uint32_t hw = act_bits(tx) | (act_bits(ty) << 16);
+        const float2 hv2 = Act::from_pair(hw);
+        const float rx = tx - hv2.x, ry = ty - hv2.y;
+        const uint32_t mw = act_bits(rx) | (act_bits(ry) << 16);
+        const float2 mv2 = Act::from_pair(mw);
+        const uint32_t lw = act_bits(rx - mv2.x) | (act_bits(ry - mv2.y) << 16);
+        *(uint32_t*)(hl + kHT0 + 4 * lane) = hw;
+        *(uint32_t*)(hl + kHT0 + 256 + 4 * lane) = mw;
+        *(uint32_t*)(hl + kHT0 + 512 + 4 * lane) = lw;
+        if (lane == 0) ((float*)(hl + kHLam))[1] = t0s;
+      } else {
+        // flush factors (kernel:177-242 in matrix form):
+        //   pre_t = prod_{x<=t} gamma_x,  post_t = beta_t prod_{x>t} gamma_x,
+        //   M[t][s] = beta_s prod_{s<x<=t} gamma_x G[s][t] (s < t < n), R = (I + M)^-1
+        const float pre = row_prefix_prod(gam);
+        const float post = bet * suf_ex;
+        if (lane < NT) ((float4*)(hl + kHFac))[lane] = make_float4(on ? pre : 0.f, on ? post : 0.f, dq, 0.f);
+        // M (lane = column s; the gammas by readlane)
+        float* Mm = (float*)(hl + kHM);
+        {
+          float run = 1.f;
+#pragma unroll
+          for (int t = 0; t < NT; ++t) {
+            const float gt = rdl(gam, t);
+            run = t > l16 ? run * gt : run;
+            if (lane < NT) Mm[t * NT + lane] = (l16 < t && t < n) ? bet * run * gcol[t] : 0.f;
+          }
+        }
+        // R by forward substitution, lane = column c:
+        // R[t][c] = delta_tc - sum_{s<t} M[t][s] R[s][c]
+        float r[NT];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          float x = (t == l16) ? 1.f : 0.f;
+#pragma unroll
+          for (int s4 = 0; s4 < t; s4 += 4) {
+            const float4 m4 = *(const float4*)(Mm + t * NT + s4);
+            x = fmaf(-m4.x, r[s4], x);
+            if (s4 + 1 < t) x = fmaf(-m4.y, r[s4 + 1], x);
+            if (s4 + 2 < t) x = fmaf(-m4.z, r[s4 + 2], x);
+            if (s4 + 3 < t) x = fmaf(-m4.w, r[s4 + 3], x);
+          }
+          r[t] = x;
+        }
+        if (lane < NT) {
+          float* Rj = (float*)(hl + kHR);
+#pragma unroll
+          for (int t = 0; t < NT; ++t) Rj[t * NT + lane] = (t < n && on) ? r[t] : 0.f;
+        }
+      }
+    }
+    // everything is in LDS before the barrier
+    GDNR_WAIT_LGKM0();
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    return;
+  }
+
+  // ================= row waves ====================================================
+  constexpr int RPW = 16 * TPW;  // V-rows per wave
+  constexpr int VB = TPW / 2;     // vblocks (32 rows) per wave
+  const int wr = (w - U) - u * rpu;
+  const int j = uni(wr / NWH), part = wr - j * NWH;  // value head in the unit, row block of it
+  // (barrier 1: every chain wave's requests go first)
+  GDNR_COMPILER_FENCE();
+  __builtin_amdgcn_s_barrier();
+  GDNR_COMPILER_FENCE();
+  const int hv = hv0 + j;
+  const int R0 = RPW * part;
+  const uint8_t* hl = ul + kLHeads + j * kHeadLds;
+  // ---- checkpoint rows of the wave's tiles (preloaded arguments only)
+  uint8_t* ck_rows = ckpt + (bs * ck_b + hv * ck_h + R0 * ck_v);
+  u32x4_t cw[TPW][2];
+#pragma unroll
+  for (int i = 0; i < TPW; ++i) {
+    const uint32_t off = (uint32_t)(32 * (i >> 1) + 2 * l16 + (i & 1)) * ck_v + 16 * q4;
+    cw[i][0] = *(g_u32x4*)(ck_rows + off);
+    cw[i][1] = *(g_u32x4*)(ck_rows + off + 64);
+  }
+  GDNR_COMPILER_FENCE();
+  int n, pos;
+  bool do_flush;
+  read_meta(n, pos, do_flush);
+  uint8_t* scale_hv = a.scale + (bs * a.sc_b + hv * a.sc_h);
+  const int vb0 = R0 / kVBlock;
+  float sct[VB];  // the vblock scales
+#pragma unroll
+  for (int p = 0; p < VB; ++p) sct[p] = f16_bits_to_f32(ld_u16_uniform(scale_hv + (vb0 + p) * a.sc_v));
+  // v rows of the filled slots: lane (nn, q4), token t = 4 q4 + e, rows
+  // (32 p + 2 nn, 32 p + 2 nn + 1) of vblock p; the new token's from
+  // mixed_qkv; slots at or past the fill re-read slot 0 (dropped below)
+  uint32_t vp[4][VB];
+  {
+    const uint8_t* vbase = a.v + (bs * a.v_b + hv * a.v_h + (R0 + 2 * l16) * ES);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int t = 4 * q4 + e;
+      const uint8_t* src = vbase + (uint32_t)(t < n ? t : 0) * a.v_t;
+      if constexpr (FUSED)
+        if (t == pos) src = a.mixed + (b * a.mx_b + (2 * a.H * K + hv * a.V + R0 + 2 * l16) * ES);
+#pragma unroll
+      for (int p = 0; p < VB; ++p) vp[e][p] = ld32(src + 64 * p);
+    }
+  }
+  GDNR_COMPILER_FENCE();
+  // the chain wave's LDS blocks are complete after the barrier
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+
+  // ring append of the new token's v rows (full contract; this wave's rows,
+  // which no other wave reads): lanes of group q4 == pos / 4 hold them
+  if constexpr (FUSED) {
+    if (pos >= 0 && q4 == (pos >> 2)) {
+      const int e = pos & 3;
+      uint8_t* vw = a.v + (bs * a.v_b + (uint32_t)pos * a.v_t + hv * a.v_h + (R0 + 2 * l16) * ES);
+#pragma unroll
+      for (int p = 0; p < VB; ++p)
+        *(uint32_t*)(vw + 64 * p) = e == 0 ? vp[0][p] : e == 1 ? vp[1][p] : e == 2 ? vp[2][p] : vp[3][p];
+    }
+  }
+  // v of token 4 q4 + e for tile i (zero at or past the fill)
+  auto vval = [&](int i, int e) {
+    const uint32_t wv = vp[e][i >> 1];
+    const float x = act_val((i & 1) ? (wv >> 16) : wv);
+    return (4 * q4 + e) < n ? x : 0.f;
+  };
+  uint8_t* out_rows = a.out + (b * a.o_b + hv * a.o_h + R0 * ES);
+  // o of tiles 4 g .. 4 g + 3 from per-tile partials: lane (l16, q4) stores
+  // the row of tile 4 g + q4
+  auto store_out = [&](int g, float p0, float p1, float p2, float p3) {
+    float o = rows_reduce_scatter(p0, p1, p2, p3);
+    asm volatile("" : "+v"(o));  // (no tail shared between the branches)
+    Act::st(out_rows, 64 * g + 32 * (q4 >> 1) + 2 * l16 + (q4 & 1), o * a.out_scale);
+  };
+
+  if (!do_flush) {
+    // ---- replay: o = (scale S_0 T_0 + sum_t c_t v_t) K^-1/2 ---------------------------
+    // T_0 enters as the A operand rows 0 (hi), 1 (mid) and 2 (lo), the other
+    // rows zero: lanes q4 == 0 get (S_0 T_0)[row] as the sum of their first
+    // three outputs
+    const uint8_t* arow = hl + kHT0 + 256 * (l16 < 3 ? l16 : 0) + 32 * q4;
+    const float4 cc = *(const float4*)(hl + kHCoef + 16 * q4);
+    const float t0s = ((const float*)(hl + kHLam))[1];
+    // (the codes taken afresh: no conversion here is shared with the flush
+    // branch, so none is hoisted above the branch)
+#pragma unroll
+    for (int i = 0; i < TPW; ++i) asm volatile("" : "+v"(cw[i][0]), "+v"(cw[i][1]));
+    float part_[TPW];
+#pragma unroll
+    for (int i = 0; i < TPW; ++i) {
+      f32x4_t c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const u32x4_t x = *(const u32x4_t*)(arow + 128 * (m >> 1) + 16 * (m & 1));
+        c = mfma16(l16 < 3 ? x : u32x4_t{0u, 0u, 0u, 0u}, codes8(cw[i], m), c);
+      }
+      float wsum = cc.x * vval(i, 0);
+      wsum = fmaf(cc.y, vval(i, 1), wsum);
+      wsum = fmaf(cc.z, vval(i, 2), wsum);
+      wsum = fmaf(cc.w, vval(i, 3), wsum);
+      part_[i] = fmaf(c[0] + (c[1] + c[2]), sct[i >> 1] * t0s, wsum);
+    }
+#pragma unroll
+    for (int g = 0; g < TPW / 4; ++g) store_out(g, part_[4 * g], part_[4 * g + 1], part_[4 * g + 2], part_[4 * g + 3]);
+    return;
+  }
+
+  // registers are short in the flush: the v rows wait in LDS (read per tile)
+  uint8_t* vl = ul + kUnitBase + (wr * 64 + lane) * 16 * VB;
+#pragma unroll
+  for (int p = 0; p < VB; ++p) *(u32x4_t*)(vl + 16 * p) = u32x4_t{vp[0][p], vp[1][p], vp[2][p], vp[3][p]};
+  asm volatile("" ::: "memory");
+  auto vval_l = [&](int i, int e) {
+    const uint32_t wv = *(const uint32_t*)(vl + 16 * (i >> 1) + 4 * e);
+    const float x = act_val((i & 1) ? (wv >> 16) : wv);
+    return (4 * q4 + e) < n ? x : 0.f;
+  };
+  // ---- flush, one vblock (tiles 2p, 2p + 1) at a time: P = X S_0^T of its
+  // rows on every ring token, W = v - pre P, U = R W, U~ = post U, then
+  // S_n = lam S_0 + K^T U~ by 16 x 4 column groups in two passes: the vblock
+  // amax and o = S_n q, then the requantisation in place
+  const float lam = ((const float*)(hl + kHLam))[0];
+  float opart[TPW];
+  // S_n column group ct of tile i: lane (nn, q4) gets
+  // S_n[row r(i, nn)][64 (ct / 4) + 16 q4 + 4 (ct % 4) + e], byte 4 (ct % 4) + e
+  // of its code chunk ct / 4. lam S_0 enters through the MFMA as
+  // (ls I) S_0^T with ls = lam * scale split into hi + lo halves; each hi/lo
+  // pair is one 16x16x32 MFMA (k-slots 8 q4 + j: j < 4 the hi part, j >= 4
+  // the lo part of token / column 4 q4 + (j & 3)).
+  auto a_ls_of = [&](int p) {
+    const float ls = lam * sct[p];
+    uint32_t hb, lb;
+    if constexpr (kBF16) {
+      hb = f32_to_bf16(ls);
+      lb = f32_to_bf16(ls - __uint_as_float(hb << 16));
+    } else {
+      const _Float16 hh = (_Float16)ls;
+      hb = __builtin_bit_cast(uint16_t, hh);
+      lb = __builtin_bit_cast(uint16_t, (_Float16)(ls - (float)hh));
+    }
+    const uint32_t d0 = l16 == 4 * q4 ? 0xFFFFu : 0u, d1 = l16 == 4 * q4 + 1 ? 0xFFFF0000u : 0u;
+    const uint32_t d2 = l16 == 4 * q4 + 2 ? 0xFFFFu : 0u, d3 = l16 == 4 * q4 + 3 ? 0xFFFF0000u : 0u;
+    const uint32_t h2 = hb | (hb << 16), l2 = lb | (lb << 16);
+    return u32x4_t{h2 & (d0 | d1), h2 & (d2 | d3), l2 & (d0 | d1), l2 & (d2 | d3)};
+  };
+  auto s_group = [&](int i, int ct, const u32x4_t& a_ls, const u32x4_t& pk) {
+    uint32_t cword = cw[i][ct >> 2][ct & 3];
+    asm volatile("" : "+v"(cword));  // converted again at every use (no register kept)
+    const uint2 c2 = codes4(cword);
+    const f32x4_t z = {0.f, 0.f, 0.f, 0.f};
+    const f32x4_t s0 = mfma16(a_ls, u32x4_t{c2.x, c2.y, c2.x, c2.y}, z);
+    int ko = kLKT + 2 * ((ct * 16 + l16) * 16 + 4 * q4);
+    asm volatile("" : "+v"(ko));  // read again at every use (no register kept)
+    const uint2 k2 = *(const uint2*)(ul + ko);
+    return mfma16(u32x4_t{k2.x, k2.y, k2.x, k2.y}, pk, s0);
+  };
+#pragma unroll
+  for (int p = 0; p < VB; ++p) {
+    u32x4_t packed[2];
+#pragma unroll
+    for (int ii = 0; ii < 2; ++ii) {
+      const int i = 2 * p + ii;
+      f32x4_t pr = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const u32x4_t x =
+            *(const u32x4_t*)(ul + kLX + l16 * kXStride + 128 * (m >> 1) + 16 * (m & 1) + 32 * q4);
+        pr = mfma16(x, codes8(cw[i], m), pr);
+      }
+      float wv[4], post[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int t = 4 * q4 + e;
+        const float2 fc = *(const float2*)(hl + kHFac + 16 * t);
+        post[e] = fc.y;
+        wv[e] = t < n ? vval_l(i, e) - fc.x * (pr[e] * sct[p]) : 0.f;
+      }
+      const float4 rr = *(const float4*)(hl + kHR + 4 * (l16 * NT + 4 * q4));
+      const float rrv[4] = {rr.x, rr.y, rr.z, rr.w};
+      f32x4_t u = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) u = __builtin_amdgcn_mfma_f32_16x16x4f32(rrv[e], wv[e], u, 0, 0, 0);
+      float ut[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ut[e] = u[e] * post[e];
+      if constexpr (kBF16) {
+        // hi/lo split: U~ = hi + lo to ~16 bits, both halves bf16 operands
+        const uint32_t h01 = pack_bf16x2(ut[0], ut[1]), h23 = pack_bf16x2(ut[2], ut[3]);
+        const uint32_t l01 =
+            pack_bf16x2(ut[0] - __uint_as_float(h01 << 16), ut[1] - __uint_as_float(h01 & 0xFFFF0000u));
+        const uint32_t l23 =
+            pack_bf16x2(ut[2] - __uint_as_float(h23 << 16), ut[3] - __uint_as_float(h23 & 0xFFFF0000u));
+        packed[ii] = u32x4_t{h01, h23, l01, l23};
+      } else {
+        _Float16 hh[4], ll[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          hh[e] = (_Float16)ut[e];
+          ll[e] = (_Float16)(ut[e] - (float)hh[e]);
+        }
+        auto pk = [](_Float16 x, _Float16 y) {
+          return (uint32_t)__builtin_bit_cast(uint16_t, x) | ((uint32_t)__builtin_bit_cast(uint16_t, y) << 16);
+        };
+        packed[ii] = u32x4_t{pk(hh[0], hh[1]), pk(hh[2], hh[3]), pk(ll[0], ll[1]), pk(ll[2], ll[3])};
+      }
+      // one tile at a time (the second tile's products are not issued ahead)
+      asm volatile("" : "+v"(packed[ii]));
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // pass 1: the vblock amax (|x| max, NaN propagating like torch.amax) and
+    // the output partials o = S_n q over the lane's columns
+    float am = 0.f;
+    float op0 = 0.f, op1 = 0.f;
+    {
+      const u32x4_t a_ls = a_ls_of(p);
+#pragma unroll
+      for (int ct = 0; ct < 8; ++ct) {
+        const uint2 qb = *(const uint2*)(ul + kLQK + 128 * (ct >> 2) + 32 * q4 + 8 * (ct & 3));
+        const float2 qa = Act::from_pair(qb.x), qc = Act::from_pair(qb.y);
+        const f32x4_t s0 = s_group(2 * p, ct, a_ls, packed[0]);
+        const f32x4_t s1 = s_group(2 * p + 1, ct, a_ls, packed[1]);
+        am = __builtin_elementwise_maximum(am, __builtin_elementwise_maximum(__builtin_fabsf(s0[0]), __builtin_fabsf(s0[1])));
+        am = __builtin_elementwise_maximum(am, __builtin_elementwise_maximum(__builtin_fabsf(s0[2]), __builtin_fabsf(s0[3])));
+        am = __builtin_elementwise_maximum(am, __builtin_elementwise_maximum(__builtin_fabsf(s1[0]), __builtin_fabsf(s1[1])));
+        am = __builtin_elementwise_maximum(am, __builtin_elementwise_maximum(__builtin_fabsf(s1[2]), __builtin_fabsf(s1[3])));
+        op0 = fmaf(s0[0], qa.x, op0);
+        op0 = fmaf(s0[1], qa.y, op0);
+        op0 = fmaf(s0[2], qc.x, op0);
+        op0 = fmaf(s0[3], qc.y, op0);
+        op1 = fmaf(s1[0], qa.x, op1);
+        op1 = fmaf(s1[1], qa.y, op1);
+        op1 = fmaf(s1[2], qc.x, op1);
+        op1 = fmaf(s1[3], qc.y, op1);
+        // one column group at a time: the products of later groups are not
+        // issued ahead (each would hold four more registers)
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    // computed here, not sunk to the output: their inputs die here
+    asm volatile("" : "+v"(op0), "+v"(op1));
+    opart[2 * p] = op0;
+    opart[2 * p + 1] = op1;
+    const uint32_t amb = wave_max_u32(__float_as_uint(am));
+    // the reference quantiser (ref:36-37,83-99): s = amax / 448 (1 when amax
+    // is not > 0); codes = e4m3fn(clamp(x / s, +-448)) with the unrounded s;
+    // the quotient by quotient_rn when the block is finite
+    const float amax = __uint_as_float(amb);
+    const float s32 = (amax > 0.0f) ? amax / 448.0f : 1.0f;
+    const bool fast = quotient_fast(amb, s32);
+    const float rcp = 1.0f / s32;
+    // pass 2: the same column groups again, requantised and stored (the
+    // division path of non-finite or tiny-scale blocks is a loop of its own)
+    auto pass2 = [&](auto quant) {
+      const u32x4_t a_ls = a_ls_of(p);
+#pragma unroll
+      for (int ii = 0; ii < 2; ++ii) {
+        const int i = 2 * p + ii;
+        const uint32_t ro = (uint32_t)(32 * p + 2 * l16 + ii) * ck_v + 16 * q4;
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          uint32_t wd[4];
+#pragma unroll
+          for (int w4 = 0; w4 < 4; ++w4) wd[w4] = quant(s_group(i, 4 * hh + w4, a_ls, packed[ii]));
+          *(g_u32x4_w*)(ck_rows + ro + 64 * hh) = u32x4_t{wd[0], wd[1], wd[2], wd[3]};
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    };
+    if (uni((int)fast) != 0) {
+      pass2([&](const f32x4_t& v) {
+        return f32x4_to_fp8(quotient_rn(v[0], s32, rcp), quotient_rn(v[1], s32, rcp), quotient_rn(v[2], s32, rcp),
+                            quotient_rn(v[3], s32, rcp));
+      });
+    } else {
+      // (one quotient at a time: this path is rare and should hold few registers)
+      pass2([&](const f32x4_t& v) {
+        __builtin_amdgcn_sched_barrier(0);
+        float qv[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          qv[e] = v[e] / s32;
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        const uint32_t wd = f32x4_to_fp8_ref(qv[0], qv[1], qv[2], qv[3]);
+        __builtin_amdgcn_sched_barrier(0);
+        return wd;
+      });
+    }
+    if (lane == 0) *(uint16_t*)(scale_hv + (vb0 + p) * a.sc_v) = __builtin_bit_cast(uint16_t, (_Float16)s32);
+  }
+#pragma unroll
+  for (int g = 0; g < TPW / 4; ++g) store_out(g, opart[4 * g], opart[4 * g + 1], opart[4 * g + 2], opart[4 * g + 3]);
+}
+
+template <int TPW, int NWH, bool FUSED, bool GATE_F32, bool SLOTS>
+int launch_variant(const StepArgs& a, hipStream_t s) {
+  const dim3 grid((unsigned)(a.H * (a.G / a.gw) / a.units), (unsigned)a.B),
+      block((unsigned)(64 * a.units * (1 + a.gw * NWH)));
+  auto kernel = decode_kernel<TPW, NWH, FUSED, GATE_F32, SLOTS>;
+  if (a.lds_bytes > 64 * 1024) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, a.lds_bytes);
+    if (e != hipSuccess) return (int)e;
+  }
+  hipLaunchKernelGGL(kernel, grid, block, a.lds_bytes, s, a.ckpt, a.k, a.ck_b, a.ck_h, a.ck_v, a.k_b, a.k_t, a.k_h,
+                     a.L, a.G, a.gw | (a.units << 8), a);
+  return 0;
+}
+
+template <int TPW, int NWH>
+int launch_shape(const StepArgs& a, bool fused, bool gate_f32, hipStream_t s) {
+  if (!fused) return launch_variant<TPW, NWH, false, false, false>(a, s);
+  if (a.slot && gate_f32) return launch_variant<TPW, NWH, true, true, true>(a, s);
+  if (a.slot) return launch_variant<TPW, NWH, true, false, true>(a, s);
+  if (gate_f32) return launch_variant<TPW, NWH, true, true, false>(a, s);
+  return launch_variant<TPW, NWH, true, false, false>(a, s);
+}
+
+}  // namespace
+
+#if GDNR_ACT == 0
+// LDS bytes of the decode kernel for gw value heads (of nwh row waves each;
+// the layout is the same for both activation dtypes)
+int32_t decode_lds_bytes(int32_t units, int32_t row_waves, int32_t vblocks) {
+  return units * unit_lds(row_waves, vblocks);
+}
+#endif
+
+int GDNR_SUFFIX(launch_decode)(const StepArgs& a, bool fused, bool gate_f32, void* stream) {
+  hipStream_t s = (hipStream_t)stream;
+  int rc;
+  // V = 64 a.sw: one wave of 64 rows per value head; 128: one of 128 rows; 256: two
+  if (a.sw == 1) rc = launch_shape<4, 1>(a, fused, gate_f32, s);
+  else if (a.sw == 2) rc = launch_shape<8, 1>(a, fused, gate_f32, s);
+  else rc = launch_shape<8, 2>(a, fused, gate_f32, s);
+  if (rc) return rc;
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? 0 : (int)e;
+}
+
+}  // namespace gdnr
+
+#endif  // GDNR_ACT != 2

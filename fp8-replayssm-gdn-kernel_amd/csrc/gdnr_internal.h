@@ -57,6 +57,7 @@ struct ReplayArgs {
   // workgroup, V-rows per wave, the new token's k row, per-head publish
   // flags, coefficients and [17 x 17] Gram matrices
   int32_t sw, rpw, lds_knew, lds_flag, lds_c, lds_g;
+  int32_t units;  // decode kernel: (key head, value-head group) units per workgroup
   // flush (MFMA rebuild), per head: R = (I + M)^-1 [16 x 16] f32, per-token
   // factors (pre, post, dq, -) f32, lam_all f32; K^T operand tiles [K x 16]
   // in the ring dtype; per-head scratch (3 KiB)
@@ -81,13 +82,15 @@ struct StepArgs {
   uint32_t ck_b, ck_h, ck_v, sc_b, sc_h, sc_v, q_b, q_h, k_b, k_t, k_h, v_b, v_t, v_h;
   uint32_t g_b, g_t, g_h, be_b, be_t, be_h, vl_s, fl_s, pos_s, o_b, o_h, mx_b;
   uint32_t a_b, a_h, bg_b, bg_h, al_s, db_s, qo_b, qo_h;
-  int32_t B, H, G, V, L, gw, block_v, n_vt, sw, rpw;
+  int32_t B, H, G, V, L, gw, block_v, n_vt, sw, rpw, units;
   float out_scale;
   int32_t lds_q, lds_knew, lds_k, lds_flag, lds_c, lds_t, lds_g, lds_v, lds_r, lds_fac, lds_kt, lds_lam, lds_u, lds_bytes;
   // slot indirection (fused step only): sequence b's checkpoint, scale and
   // ring rows are those of slot slot[b] (int32, clamped to [0, n_slots));
   // nullptr: slot b
   const uint8_t* slot; uint32_t sl_s; int32_t n_slots;
+  // device word counting bounded waits that gave up (status_word())
+  uint32_t* status;
 };
 
 struct PrepArgs {
@@ -163,6 +166,17 @@ GDNR_DECLARE_LAUNCHERS(bf16)
 GDNR_DECLARE_LAUNCHERS(f16)
 GDNR_DECLARE_LAUNCHERS(f32)
 #undef GDNR_DECLARE_LAUNCHERS
+// decode kernel (gdnr_decode.hip): 16-bit activations, rings of <= 16 tokens,
+// V % 64 == 0; StepArgs.gw value heads per workgroup, StepArgs.sw = V / 64
+// waves per value head
+int launch_decode_bf16(const StepArgs& a, bool fused, bool gate_f32, void* stream);
+int launch_decode_f16(const StepArgs& a, bool fused, bool gate_f32, void* stream);
+int32_t decode_lds_bytes(int32_t units, int32_t row_waves, int32_t vblocks);
+// the device word of the current device that counts bounded waits which gave
+// up (nullptr if the symbol cannot be resolved), and its host read-out
+uint32_t* status_word();
+int read_status(uint32_t* count, bool reset);
+int device_cus();
 int launch_quantize(const QuantArgs& a, void* stream);
 int launch_rmw_step(const RmwArgs& a, int state_dt, int act_dt, void* stream);
 int launch_rmw_packed(const RmwArgs& a, int state_dt, int act_dt, bool gate_f32, void* stream);

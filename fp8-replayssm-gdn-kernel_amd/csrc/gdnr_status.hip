@@ -1,0 +1,53 @@
+// gdnr_status.hip -- the device word through which kernels report bounded
+// waits that gave up (an LDS flag never raised), and its host read-out.
+//
+// One word per device (a file-scope __device__ variable: every GPU that
+// loads the library holds its own copy). Kernels add to it with a global
+// atomic; the host reads and optionally clears it with gdnr_wait_timeouts().
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "gdnr_internal.h"
+
+namespace gdnr {
+
+__device__ uint32_t wait_status_word[1];
+
+namespace {
+constexpr int kMaxDevices = 64;
+uint32_t* g_status_ptr[kMaxDevices] = {};
+}  // namespace
+
+uint32_t* status_word() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  if (!g_status_ptr[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(wait_status_word)) != hipSuccess) return nullptr;
+    g_status_ptr[dev] = (uint32_t*)p;  // the same address on every call: a benign race between threads
+  }
+  return g_status_ptr[dev];
+}
+
+int read_status(uint32_t* count, bool reset) {
+  uint32_t* p = status_word();
+  if (!p) return (int)hipErrorInvalidSymbol;
+  hipError_t e = hipMemcpy(count, p, sizeof(uint32_t), hipMemcpyDeviceToHost);
+  if (e == hipSuccess && reset) e = hipMemset(p, 0, sizeof(uint32_t));
+  if (e == hipSuccess) e = hipDeviceSynchronize();
+  return (int)e;
+}
+
+// compute units of the current device (cached per device; 256 if the query fails)
+int device_cus() {
+  static int cus[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cus[dev]) {
+    int n = 0;
+    cus[dev] = (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0) ? n : 256;
+  }
+  return cus[dev];
+}
+
+}  // namespace gdnr

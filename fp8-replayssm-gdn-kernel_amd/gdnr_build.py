@@ -5,7 +5,7 @@
 Objects go to _build/ next to this file; the library is written in-tree
 (next to this file) so it travels with the source tree to the GPU host.
 The C-ABI validation layer (csrc/gdnr_abi.cpp) is plain C++ compiled by g++;
-the kernels (csrc/gdnr_kernels.hip) by hipcc. Packed-FP32 VALU instructions
+the kernels (csrc/*.hip) by hipcc. Packed-FP32 VALU instructions
 are disabled for all device code.
 """
 
@@ -33,8 +33,11 @@ DEVICE_FLAGS = [
 ]
 HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra"]
 ACTS = ("bf16", "f16", "f32")  # activation dtypes, one kernel object each (GDNR_ACT = index)
-KERNEL_SOURCES = ("gdnr_kernels", "gdnr_step")  # compiled once per activation dtype
-SINGLE_SOURCES = ("gdnr_rmw", "gdnr_formats")   # compiled once (dtypes are template arguments)
+KERNEL_SOURCES = ("gdnr_kernels", "gdnr_step", "gdnr_decode")  # compiled once per activation dtype
+SINGLE_SOURCES = ("gdnr_rmw", "gdnr_formats", "gdnr_status")  # compiled once (dtypes are template arguments)
+# per-source device flags: the decode kernel's first 13 argument dwords are
+# preloaded into SGPRs at wave launch (gfx950 kernarg preload)
+SOURCE_FLAGS = {"gdnr_decode": ["-mllvm", "-amdgpu-kernarg-preload-count=13"]}
 
 
 def _run(cmd: list[str], verbose: bool) -> None:
@@ -57,7 +60,8 @@ def build(verbose: bool = False) -> Path:
         for i, act in enumerate(ACTS):
             obj = BUILD_DIR / f"{src}_{act}.o"
             kern_objs.append(obj)
-            jobs.append([HIPCC, *DEVICE_FLAGS, *inc, f"-DGDNR_ACT={i}", "-c", str(CSRC / f"{src}.hip"), "-o", str(obj)])
+            jobs.append([HIPCC, *DEVICE_FLAGS, *SOURCE_FLAGS.get(src, []), *inc, f"-DGDNR_ACT={i}", "-c",
+                         str(CSRC / f"{src}.hip"), "-o", str(obj)])
     for src in SINGLE_SOURCES:
         obj = BUILD_DIR / f"{src}.o"
         kern_objs.append(obj)
@@ -80,8 +84,8 @@ def device_assembly(act: str = "bf16", src: str = "gdnr_step", out: Path | None 
     activation dtype (inspection of waits, VGPR counts, instruction mix)."""
     out = out or BUILD_DIR / f"{src}_{act}.s"
     BUILD_DIR.mkdir(exist_ok=True)
-    _run([HIPCC, *DEVICE_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", f"-DGDNR_ACT={ACTS.index(act)}", "--cuda-device-only",
-          "-S", str(CSRC / f"{src}.hip"), "-o", str(out)], verbose)
+    _run([HIPCC, *DEVICE_FLAGS, *SOURCE_FLAGS.get(src, []), f"-I{INCLUDE}", f"-I{CSRC}",
+          f"-DGDNR_ACT={ACTS.index(act)}", "--cuda-device-only", "-S", str(CSRC / f"{src}.hip"), "-o", str(out)], verbose)
     return out
 
 

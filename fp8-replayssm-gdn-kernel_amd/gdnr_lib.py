@@ -88,6 +88,8 @@ def load_library(path: Path | None = None) -> ctypes.CDLL:
     lib.gdnr_last_error.argtypes = []
     lib.gdnr_abi_version.restype = ctypes.c_int
     lib.gdnr_abi_version.argtypes = []
+    lib.gdnr_wait_timeouts.restype = ctypes.c_int
+    lib.gdnr_wait_timeouts.argtypes = [ctypes.POINTER(ctypes.c_uint32), ctypes.c_int32]
     for name, (n_tensors, n_ints, *n_floats) in ENTRY_POINTS.items():
         fn = getattr(lib, name)
         fn.restype = ctypes.c_int
@@ -132,3 +134,16 @@ def call(name: str, tensors, ints=(), stream: int | None = None, floats=()) -> N
 
 def current_stream(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
+
+
+def wait_timeouts(reset: bool = False) -> int:
+    """Bounded LDS waits of the decode kernels that gave up on the current
+    device since the last reset (gdnr_wait_timeouts; synchronises the device).
+    Nonzero means some step's output is meaningless and its workgroup skipped
+    its in-place checkpoint stores."""
+    lib = load_library()
+    count = ctypes.c_uint32(0)
+    status = lib.gdnr_wait_timeouts(ctypes.byref(count), 1 if reset else 0)
+    if status != 0:
+        raise GdnrError(status, lib.gdnr_last_error().decode())
+    return int(count.value)

@@ -78,6 +78,18 @@ const char* gdnr_last_error(void);
 int gdnr_abi_version(void);
 
 /*
+ * Diagnostics of the decode kernels' bounded waits. Inside a workgroup the
+ * waves of a value head hand the coefficient chain to each other through an
+ * LDS flag, and every such wait is bounded (2^22 polls). A wait that gives
+ * up adds 1 to a per-device status word and the workgroup skips its
+ * in-place checkpoint and scale stores (its output is then meaningless).
+ * *count receives the current device's word; reset != 0 clears it. This
+ * call synchronises the device (it copies the word to the host).
+ * No counterpart in the reference (its Triton kernels have no inter-wave waits).
+ */
+int gdnr_wait_timeouts(uint32_t* count, int32_t reset);
+
+/*
  * One decode step of the replay, per sequence b:
  *   flush[b] == 0: adjoint replay of ring tokens [0, valid_len[b]) against the
  *                  dequantised checkpoint; writes out[b] only.

@@ -32,6 +32,20 @@ def device():
     return torch.device("cuda:0")
 
 
+@pytest.fixture(autouse=True)
+def _no_wait_timeouts(request):
+    """Every GPU test ends with the device's bounded-wait status word at zero:
+    no decode workgroup gave up waiting for its coefficient chain."""
+    if request.node.get_closest_marker("gpu") is None:
+        yield
+        return
+    import gdnr_lib
+
+    gdnr_lib.wait_timeouts(reset=True)
+    yield
+    assert gdnr_lib.wait_timeouts(reset=True) == 0, "a decode kernel's bounded wait gave up"
+
+
 def rel_l2(actual, expected) -> float:
     a = np.asarray(actual, dtype=np.float64)
     e = np.asarray(expected, dtype=np.float64)

@@ -114,18 +114,27 @@ def test_replay_matches_oracle(device, block_v):
 
 
 def test_replay_block_v_and_split_identical(device):
-    """Tilings and the two-launch split give bit-identical outputs."""
+    """The tilings (one decode kernel) give bit-identical outputs, and so do
+    the two precompute variants of the two-launch split; the split (T_0 in
+    f32, then S_0 T_0) and the one-launch decode (T_0 as three 16-bit MFMA
+    rows) sum in different orders and differ by at most one bf16 ulp."""
     case = make_replay_case(4, 8, device, seed=4)
     outs = [run_replay(case, block_v=bv) for bv in (32, 64, 128)]
+    for o in outs[1:]:
+        assert torch.equal(o, outs[0])
     B, L = 4, 8
     tq = torch.empty(B, 32, 128, dtype=torch.float32, device=device)
     coef = torch.zeros(B, 32, L, dtype=torch.float32, device=device)
+    split = []
     for grouped in (True, False):
-        outs.append(gk.gdn_replay_fp8_split(case["ckpt"].payload, case["ckpt"].scale, case["q"], case["k"],
-                                            case["v"], case["g"], case["beta"], case["valid"], tq, coef,
-                                            block_v=128, precompute_grouped=grouped))
-    for o in outs[1:]:
-        assert torch.equal(o, outs[0])
+        split.append(gk.gdn_replay_fp8_split(case["ckpt"].payload, case["ckpt"].scale, case["q"], case["k"],
+                                             case["v"], case["g"], case["beta"], case["valid"], tq, coef,
+                                             block_v=128, precompute_grouped=grouped))
+    assert torch.equal(split[1], split[0])
+    fused, two = np32(outs[0]).ravel(), np32(split[0]).ravel()
+    ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(two), 1e-30))) - 7)  # bf16 spacing at |two|
+    assert np.all(np.abs(fused - two) <= ulp), np.max(np.abs(fused - two) / ulp)
+    assert np.mean(fused != two) < 0.01
     _, tq_ref, coef_ref = gdn_oracle.adjoint_replay(
         gdn_oracle.dequantize_vblock32(codes_np(case["ckpt"].payload), case["ckpt"].scale.cpu().numpy()),
         np32(case["q"]), np32(case["k"]), np32(case["v"]), np32(case["g"]), np32(case["beta"]),
