@@ -39,6 +39,7 @@
 //
 // Compiled once per 16-bit activation dtype (GDNR_ACT = 0 bf16, 1 f16).
 #include <hip/hip_runtime.h>
+#include <stddef.h>
 #include <stdint.h>
 
 #include <type_traits>
@@ -101,6 +102,13 @@ __device__ __forceinline__ float rdl(float x, int lane) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), lane));
 }
 __device__ __forceinline__ int uni(int x) { return __builtin_amdgcn_readfirstlane(x); }
+// a uniform value the compiler cannot see through: work derived from it
+// stays after this point (is not hoisted into code shared by the roles,
+// where it would wait for the argument block)
+__device__ __forceinline__ int opaque_s(int x) {
+  asm volatile("" : "+s"(x));
+  return x;
+}
 __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) { return (float)__builtin_bit_cast(_Float16, (uint16_t)h); }
 
 // uniform loads through the scalar cache of data this kernel does not write
@@ -123,6 +131,26 @@ __device__ __forceinline__ uint8_t* opaque_uniform(uint8_t* p) {
 }
 typedef __attribute__((address_space(1))) const u32x4_t g_u32x4;
 typedef __attribute__((address_space(1))) u32x4_t g_u32x4_w;
+// The kernel's arguments as laid out in the kernarg segment (parameters in
+// order, naturally aligned), to reach the argument block by address.
+struct DecodeKernArgs {
+  uint8_t* ckpt;
+  uint8_t* kring;
+  uint32_t ck_b, ck_h, ck_v, k_b, k_t, k_h;
+  int32_t L, G, shape;
+  StepArgs a;
+};
+// The argument block through a pointer the compiler cannot see through:
+// its scalar loads issue after this point (they are not hoisted above the
+// checkpoint loads, whose address registers they could otherwise tie up).
+typedef __attribute__((address_space(4))) const StepArgs c_args;
+typedef __attribute__((address_space(4))) const uint8_t c_u8;
+__device__ __forceinline__ const StepArgs& opaque_args() {
+  uint64_t v = (uint64_t)((c_u8*)__builtin_amdgcn_kernarg_segment_ptr() + offsetof(DecodeKernArgs, a));
+  uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
+  asm volatile("" : "+s"(lo), "+s"(hi));
+  return *(const StepArgs*)(c_args*)(((uint64_t)hi << 32) | lo);
+}
 __device__ __forceinline__ uint32_t ld32(const uint8_t* p) { return *(const uint32_t*)p; }
 
 // DPP move within a 16-lane row; lanes whose source is outside the row get `fill`
@@ -130,6 +158,21 @@ template <int CTRL>
 __device__ __forceinline__ float dpp_row(float x, float fill) {
   return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, fill), __builtin_bit_cast(int, x),
                                                                CTRL, 0xF, 0xF, false));
+}
+// every lane of each 16-lane row gets lane n of its row (DPP row_newbcast)
+template <int N>
+__device__ __forceinline__ float row_bcast(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x150 + N, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float row_bcast_n(float x, int n) {
+  switch (n) {
+    case 0: return row_bcast<0>(x);   case 1: return row_bcast<1>(x);   case 2: return row_bcast<2>(x);
+    case 3: return row_bcast<3>(x);   case 4: return row_bcast<4>(x);   case 5: return row_bcast<5>(x);
+    case 6: return row_bcast<6>(x);   case 7: return row_bcast<7>(x);   case 8: return row_bcast<8>(x);
+    case 9: return row_bcast<9>(x);   case 10: return row_bcast<10>(x); case 11: return row_bcast<11>(x);
+    case 12: return row_bcast<12>(x); case 13: return row_bcast<13>(x); case 14: return row_bcast<14>(x);
+    default: return row_bcast<15>(x);
+  }
 }
 __device__ __forceinline__ float row_prefix_prod(float x) {
   x *= dpp_row<0x111>(x, 1.f);
@@ -179,8 +222,8 @@ constexpr int kHM = kHR + 1024;                // f32 [16][16]: M (chain scratch
 constexpr int kHeadLds = kHM + 1024;
 constexpr int kMaxDecodeHeads = 2;            // value heads per unit (gw)
 constexpr int kUnitBase = kLHeads + kMaxDecodeHeads * kHeadLds;  // LDS of one unit before its v rows
-// then (flush) the v rows of each of its row waves: lane l's 16 VB bytes at 16 VB l
-__host__ __device__ constexpr int unit_lds(int rpu, int vb) { return kUnitBase + rpu * 64 * 16 * vb; }
+// then the v rows of each of its row waves, token-major: [16][32 vb + 16] bytes
+__host__ __device__ constexpr int unit_lds(int rpu, int vb) { return kUnitBase + rpu * kStepRing * (64 * vb + 16); }
 
 // raw bits of a gating input (f32, or the activation dtype) and their value
 template <bool GATE_F32>
@@ -219,48 +262,66 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
   const int u = uni(chain ? w : (w - U) / rpu);  // the wave's unit
   const int r = (int)blockIdx.x * U + u;         // unit within the sequence: (key head, group)
   const int n_grp = uni(G / gw);
-  const int h = uni(r / n_grp), grp = r - h * n_grp, b = blockIdx.y;
+  const int h = uni(r / n_grp), grp = r - h * n_grp, b0 = blockIdx.y;
   const int hv0 = h * G + grp * gw;              // first value head of the unit
   uint8_t* const ul = lds + u * unit_lds(rpu, TPW / 2);  // the unit's LDS block
 
-  int bs = b;
+  int bs = b0;
   if constexpr (SLOTS) {
-    const int sl = (int)uni((int)ld_u32_uniform(a.slot + b * a.sl_s));
+    const int sl = (int)uni((int)ld_u32_uniform(a.slot + b0 * a.sl_s));
     bs = (sl >= 0 && sl < a.n_slots) ? sl : 0;
   }
-  // per-sequence metadata (scalar; needed by every wave)
-  auto read_meta = [&](int& n, int& pos, bool& do_flush) {
-    const int n_raw = (int)ld_u32_uniform(a.valid_len + b * a.vl_s);
-    int pos_raw = -1;
-    if constexpr (FUSED) pos_raw = (int)ld_u32_uniform(a.pos + b * a.pos_s);
-    uint32_t flush_word = 0, flush_shift = 0;
-    if (a.flush) {
-      const uintptr_t fa = (uintptr_t)(a.flush + b * a.fl_s);
-      flush_word = ld_u32_uniform((const void*)(fa & ~(uintptr_t)3));
-      flush_shift = 8u * (uint32_t)(fa & 3);
+  // per-sequence metadata (scalar; needed by every wave): the loads issue
+  // early, the values are decoded where they are first needed
+  struct MetaRaw {
+    int n_raw, pos_raw;
+    uint32_t flush_word, flush_shift;
+  };
+  auto load_meta = [&](const StepArgs& A, int bq) {
+    MetaRaw m{(int)ld_u32_uniform(A.valid_len + bq * A.vl_s), -1, 0u, 0u};
+    if constexpr (FUSED) m.pos_raw = (int)ld_u32_uniform(A.pos + bq * A.pos_s);
+    if (A.flush) {
+      const uintptr_t fa = (uintptr_t)(A.flush + bq * A.fl_s);
+      m.flush_word = ld_u32_uniform((const void*)(fa & ~(uintptr_t)3));
+      m.flush_shift = 8u * (uint32_t)(fa & 3);
     }
-    n = min(max(uni(n_raw), 0), L);
+    return m;
+  };
+  auto decode_meta = [&](const MetaRaw& m, int& n, int& pos, bool& do_flush) {
+    n = min(max(uni(m.n_raw), 0), L);
     pos = -1;
     if constexpr (FUSED) {
-      const int p = uni(pos_raw);
+      const int p = uni(m.pos_raw);
       pos = (p >= 0 && p < L) ? p : -1;
     }
-    do_flush = uni((int)((flush_word >> flush_shift) & 0xFFu)) != 0;
+    do_flush = uni((int)((m.flush_word >> m.flush_shift) & 0xFFu)) != 0;
+  };
+  auto read_meta = [&](const StepArgs& A, int& n, int& pos, bool& do_flush) {
+    decode_meta(load_meta(A, opaque_s(b0)), n, pos, do_flush);
   };
 
   if (chain) {
     // ================= chain wave =================================================
+    // (the sequence index through opaque_s: addresses from the argument block
+    // are formed here, not in code shared with the row waves)
+    const int b = opaque_s(b0);
+    // Lane (t = l16, row q4). For the gates, the coefficient chain and the
+    // flush factors, row j holds value head hv0 + j of the unit (rows at or
+    // past gw repeat the last head and publish nothing): the heads advance in
+    // the same instructions.
+    const int jr = q4 < gw ? q4 : gw - 1;
+    const bool pub = q4 < gw;
+    const int hvr = hv0 + jr;
     // ---- loads: the key ring in the X layout (all 16 rows; rows at or past
-    // the fill are zeroed below), the query / new-token rows, the gates of
-    // every value head of the workgroup (lane t: token t)
+    // the fill are zeroed below), the metadata, the query / new-token rows,
+    // the gates (lane (t, j): token t of head j)
     const int tl = l16 < L ? l16 : 0;
-    const uint8_t* krow = kring + (bs * k_b + h * k_h + (uint32_t)tl * k_t) + 32 * q4;
+    const uint8_t* krow = kring + (bs * k_b + h * k_h + (uint32_t)tl * k_t) + 64 * q4;
     u32x4_t xr[4];
-    xr[0] = ld16(krow);
-    xr[1] = ld16(krow + 16);
-    xr[2] = ld16(krow + 128);
-    xr[3] = ld16(krow + 144);
+#pragma unroll
+    for (int m = 0; m < 4; ++m) xr[m] = ld16(krow + 16 * m);
     GDNR_COMPILER_FENCE();
+    const MetaRaw meta = load_meta(a, b);
     uint32_t qbits, kbits = 0;
     if constexpr (FUSED) {
       const uint8_t* row = a.mixed + b * a.mx_b;
@@ -269,21 +330,15 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
     } else {
       qbits = ld32(a.q + (b * a.q_b + h * a.q_h) + 4 * lane);
     }
-    // the gates of the (at most kMaxDecodeHeads) value heads, lane t: token t
-    const int tl2 = l16 < L ? l16 : 0;
-    uint32_t g_raw[kMaxDecodeHeads], be_raw[kMaxDecodeHeads], ab_raw[kMaxDecodeHeads][2];
-    float alog[kMaxDecodeHeads], dtb[kMaxDecodeHeads];
-#pragma unroll
-    for (int j = 0; j < kMaxDecodeHeads; ++j) {
-      const int hv = hv0 + (j < gw ? j : 0);
-      g_raw[j] = *(const uint16_t*)(a.g + (bs * a.g_b + (uint32_t)tl2 * a.g_t + hv * a.g_h));
-      be_raw[j] = *(const uint16_t*)(a.beta + (bs * a.be_b + (uint32_t)tl2 * a.be_t + hv * a.be_h));
-      if constexpr (FUSED) {
-        ab_raw[j][0] = gate_bits<GATE_F32>(a.a + (b * a.a_b + hv * a.a_h));
-        ab_raw[j][1] = gate_bits<GATE_F32>(a.bgate + (b * a.bg_b + hv * a.bg_h));
-        alog[j] = *(const float*)(a.a_log + hv * a.al_s);
-        dtb[j] = *(const float*)(a.dt_bias + hv * a.db_s);
-      }
+    const uint32_t g_raw = *(const uint16_t*)(a.g + (bs * a.g_b + (uint32_t)tl * a.g_t + hvr * a.g_h));
+    const uint32_t be_raw = *(const uint16_t*)(a.beta + (bs * a.be_b + (uint32_t)tl * a.be_t + hvr * a.be_h));
+    uint32_t ab0 = 0, ab1 = 0;
+    float alog = 0.f, dtb = 0.f;
+    if constexpr (FUSED) {
+      ab0 = gate_bits<GATE_F32>(a.a + (b * a.a_b + hvr * a.a_h));
+      ab1 = gate_bits<GATE_F32>(a.bgate + (b * a.bg_b + hvr * a.bg_h));
+      alog = *(const float*)(a.a_log + hvr * a.al_s);
+      dtb = *(const float*)(a.dt_bias + hvr * a.db_s);
     }
     // (barrier 1: the chain requests of the workgroup enter the memory
     // pipeline before any checkpoint row; the row waves wait here)
@@ -292,7 +347,7 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
     GDNR_COMPILER_FENCE();
     int n, pos;
     bool do_flush;
-    read_meta(n, pos, do_flush);
+    decode_meta(meta, n, pos, do_flush);
     const bool full = n >= NT;
     // every load above is needed next; waiting for them here keeps later
     // waits from covering the ring-append stores
@@ -327,7 +382,7 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
     u32x4_t xa[4];
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
-      const int off = 128 * (m >> 1) + 16 * (m & 1) + 32 * q4;
+      const int off = 64 * q4 + 16 * m;
       const u32x4_t z = {0u, 0u, 0u, 0u};
       const u32x4_t qv = *(const u32x4_t*)(ul + kLQK + off);
       u32x4_t x = l16 < n ? xr[m] : (l16 == n ? qv : z);
@@ -350,7 +405,7 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
       f32x4_t dacc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int m = 0; m < 4; ++m) {
-        const int off = 128 * (m >> 1) + 16 * (m & 1) + 32 * q4;
+        const int off = 64 * q4 + 16 * m;
         const u32x4_t qv = *(const u32x4_t*)(ul + kLQK + off);
         dacc = mfma16(xa[m], l16 == 0 ? qv : u32x4_t{0u, 0u, 0u, 0u}, dacc);
       }
@@ -385,60 +440,63 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
       }
     }
 
-    // ---- per value head: gates, then the coefficient chain or the flush factors
-#pragma unroll
-    for (int j = 0; j < kMaxDecodeHeads; ++j) {
-      if (j >= gw) break;
-      const int hv = hv0 + j;
-      uint8_t* hl = ul + kLHeads + j * kHeadLds;
-      float gg = act_val(g_raw[j]);
-      float bb = act_val(be_raw[j]);
-      if constexpr (FUSED) {
-        // the new token's gates from the preparation formulas (kernel:534-562)
-        const float a_in = gate_value<GATE_F32>(ab_raw[j][0]), b_in = gate_value<GATE_F32>(ab_raw[j][1]);
-        const float x = a_in + dtb[j];
-        const float sp = x <= 20.0f ? logf(1.0f + expf(x)) : x;  // kernel:560, as written there
-        const float gate_new = Act::round(-expf(alog[j]) * sp);
-        const float beta_new = Act::round(1.0f / (1.0f + expf(-b_in)));
-        if (pos >= 0 && lane == 0) {
-          *(uint16_t*)(a.g + (bs * a.g_b + (uint32_t)pos * a.g_t + hv * a.g_h)) = (uint16_t)act_bits(gate_new);
-          *(uint16_t*)(a.beta + (bs * a.be_b + (uint32_t)pos * a.be_t + hv * a.be_h)) = (uint16_t)act_bits(beta_new);
-        }
-        gg = l16 == pos ? gate_new : gg;
-        bb = l16 == pos ? beta_new : bb;
+    // ---- per row (value head): gates, then the coefficient chain or the flush factors
+    uint8_t* hl = ul + kLHeads + jr * kHeadLds;
+    float gg = act_val(g_raw);
+    float bb = act_val(be_raw);
+    if constexpr (FUSED) {
+      // the new token's gates from the preparation formulas (kernel:534-562)
+      const float a_in = gate_value<GATE_F32>(ab0), b_in = gate_value<GATE_F32>(ab1);
+      const float x = a_in + dtb;
+      const float sp = x <= 20.0f ? logf(1.0f + expf(x)) : x;  // kernel:560, as written there
+      const float gate_new = Act::round(-expf(alog) * sp);
+      const float beta_new = Act::round(1.0f / (1.0f + expf(-b_in)));
+      if (pos >= 0 && l16 == 0 && pub) {
+        *(uint16_t*)(a.g + (bs * a.g_b + (uint32_t)pos * a.g_t + hvr * a.g_h)) = (uint16_t)act_bits(gate_new);
+        *(uint16_t*)(a.beta + (bs * a.be_b + (uint32_t)pos * a.be_t + hvr * a.be_h)) = (uint16_t)act_bits(beta_new);
       }
-      const float gam = on ? expf(gg) : 1.f;
-      const float bet = on ? bb : 0.f;
-      const float suf_in = row_suffix_prod(gam);
-      const float suf_ex = dpp_row<0x101>(suf_in, 1.f);
-      const float lam = rdl(suf_in, 0);
-      if (lane == 0) ((float*)(hl + kHLam))[0] = lam;
-      if (!do_flush) {
-        // s_t, t descending: acc_l = sum_{u > t} G[l][u] s_u
-        float acc = 0.f, s_mine = 0.f;
+      gg = l16 == pos ? gate_new : gg;
+      bb = l16 == pos ? beta_new : bb;
+    }
+    const float gam = on ? expf(gg) : 1.f;
+    const float bet = on ? bb : 0.f;
+    const float suf_in = row_suffix_prod(gam);
+    const float suf_ex = dpp_row<0x101>(suf_in, 1.f);
+    const float lam = row_bcast<0>(suf_in);
+    if (l16 == 0 && pub) ((float*)(hl + kHLam))[0] = lam;
+    if (!do_flush) {
+      // s_t, t descending: acc_l = sum_{u > t} G[l][u] s_u
+      float acc = 0.f, s_mine = 0.f;
 #pragma unroll
-        for (int t = NT - 1; t >= 0; --t) {
-          const float sv = rdl(bet * (dq - acc), t);
-          s_mine = l16 == t ? sv : s_mine;
-          acc = fmaf(gcol[t], sv, acc);
-        }
-        const float c = on ? s_mine * suf_ex : 0.f;
-        const float al = on ? -lam * s_mine : (l16 == n ? lam : 0.f);
-        if (lane < NT) ((float*)(hl + kHCoef))[lane] = c;
-        // T_0 = sum_t alpha_t X_t (+ lam q for a full ring) = lam (q - sum_t s_t k_t),
-        // the reference's transformed query; lane c2 holds columns 2 c2, 2 c2 + 1
+      for (int t = NT - 1; t >= 0; --t) {
+        const float sv = row_bcast_n(bet * (dq - acc), t);
+        s_mine = l16 == t ? sv : s_mine;
+        acc = fmaf(gcol[t], sv, acc);
+      }
+      const float c = on ? s_mine * suf_ex : 0.f;
+      const float al = on ? -lam * s_mine : (l16 == n ? lam : 0.f);
+      if (pub) ((float*)(hl + kHCoef))[l16] = c;
+      // T_0 = sum_t alpha_t X_t (+ lam q for a full ring) = lam (q - sum_t s_t k_t),
+      // the reference's transformed query, per head; lane c2 holds columns
+      // 2 c2, 2 c2 + 1 (the X rows are read once for the heads)
+      float2 xv[NT];
+#pragma unroll
+      for (int t = 0; t < NT; ++t) xv[t] = Act::from_pair(*(const uint32_t*)(ul + kLX + t * kXStride + 4 * lane));
+      const float2 qv = Act::from_pair(*(const uint32_t*)(ul + kLQK + 4 * lane));
+#pragma unroll
+      for (int j = 0; j < kMaxDecodeHeads; ++j) {
+        if (j >= gw) break;
         float tx = 0.f, ty = 0.f;
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-          const float at = rdl(al, t);
-          const float2 xv = Act::from_pair(*(const uint32_t*)(ul + kLX + t * kXStride + 4 * lane));
-          tx = fmaf(at, xv.x, tx);
-          ty = fmaf(at, xv.y, ty);
+          const float at = rdl(al, 16 * j + t);
+          tx = fmaf(at, xv[t].x, tx);
+          ty = fmaf(at, xv[t].y, ty);
         }
         if (full) {
-          const float2 qv = Act::from_pair(*(const uint32_t*)(ul + kLQK + 4 * lane));
-          tx = fmaf(lam, qv.x, tx);
-          ty = fmaf(lam, qv.y, ty);
+          const float lj = rdl(lam, 16 * j);
+          tx = fmaf(lj, qv.x, tx);
+          ty = fmaf(lj, qv.y, ty);
         }
         // the MFMA operand: T_0 = hi + mid + lo, three 16-bit rows (the f32
         // value to its last bits); f16 rows are scaled by a power of two
@@ -462,49 +520,50 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
         const uint32_t mw = act_bits(rx) | (act_bits(ry) << 16);
         const float2 mv2 = Act::from_pair(mw);
         const uint32_t lw = act_bits(rx - mv2.x) | (act_bits(ry - mv2.y) << 16);
-        *(uint32_t*)(hl + kHT0 + 4 * lane) = hw;
-        *(uint32_t*)(hl + kHT0 + 256 + 4 * lane) = mw;
-        *(uint32_t*)(hl + kHT0 + 512 + 4 * lane) = lw;
-        if (lane == 0) ((float*)(hl + kHLam))[1] = t0s;
-      } else {
-        // flush factors (kernel:177-242 in matrix form):
-        //   pre_t = prod_{x<=t} gamma_x,  post_t = beta_t prod_{x>t} gamma_x,
-        //   M[t][s] = beta_s prod_{s<x<=t} gamma_x G[s][t] (s < t < n), R = (I + M)^-1
-        const float pre = row_prefix_prod(gam);
-        const float post = bet * suf_ex;
-        if (lane < NT) ((float4*)(hl + kHFac))[lane] = make_float4(on ? pre : 0.f, on ? post : 0.f, dq, 0.f);
-        // M (lane = column s; the gammas by readlane)
-        float* Mm = (float*)(hl + kHM);
-        {
-          float run = 1.f;
-#pragma unroll
-          for (int t = 0; t < NT; ++t) {
-            const float gt = rdl(gam, t);
-            run = t > l16 ? run * gt : run;
-            if (lane < NT) Mm[t * NT + lane] = (l16 < t && t < n) ? bet * run * gcol[t] : 0.f;
-          }
-        }
-        // R by forward substitution, lane = column c:
-        // R[t][c] = delta_tc - sum_{s<t} M[t][s] R[s][c]
-        float r[NT];
+        uint8_t* hj = ul + kLHeads + j * kHeadLds;
+        *(uint32_t*)(hj + kHT0 + 4 * lane) = hw;
+        *(uint32_t*)(hj + kHT0 + 256 + 4 * lane) = mw;
+        *(uint32_t*)(hj + kHT0 + 512 + 4 * lane) = lw;
+        if (lane == 0) ((float*)(hj + kHLam))[1] = t0s;
+      }
+    } else {
+      // flush factors (kernel:177-242 in matrix form):
+      //   pre_t = prod_{x<=t} gamma_x,  post_t = beta_t prod_{x>t} gamma_x,
+      //   M[t][s] = beta_s prod_{s<x<=t} gamma_x G[s][t] (s < t < n), R = (I + M)^-1
+      const float pre = row_prefix_prod(gam);
+      const float post = bet * suf_ex;
+      if (pub) ((float4*)(hl + kHFac))[l16] = make_float4(on ? pre : 0.f, on ? post : 0.f, dq, 0.f);
+      // M (lane = column s; the gammas of the row by row broadcast)
+      float* Mm = (float*)(hl + kHM);
+      {
+        float run = 1.f;
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-          float x = (t == l16) ? 1.f : 0.f;
-#pragma unroll
-          for (int s4 = 0; s4 < t; s4 += 4) {
-            const float4 m4 = *(const float4*)(Mm + t * NT + s4);
-            x = fmaf(-m4.x, r[s4], x);
-            if (s4 + 1 < t) x = fmaf(-m4.y, r[s4 + 1], x);
-            if (s4 + 2 < t) x = fmaf(-m4.z, r[s4 + 2], x);
-            if (s4 + 3 < t) x = fmaf(-m4.w, r[s4 + 3], x);
-          }
-          r[t] = x;
+          const float gt = row_bcast_n(gam, t);
+          run = t > l16 ? run * gt : run;
+          if (pub) Mm[t * NT + l16] = (l16 < t && t < n) ? bet * run * gcol[t] : 0.f;
         }
-        if (lane < NT) {
-          float* Rj = (float*)(hl + kHR);
+      }
+      // R by forward substitution, lane = column c:
+      // R[t][c] = delta_tc - sum_{s<t} M[t][s] R[s][c]
+      float r[NT];
 #pragma unroll
-          for (int t = 0; t < NT; ++t) Rj[t * NT + lane] = (t < n && on) ? r[t] : 0.f;
+      for (int t = 0; t < NT; ++t) {
+        float x = (t == l16) ? 1.f : 0.f;
+#pragma unroll
+        for (int s4 = 0; s4 < t; s4 += 4) {
+          const float4 m4 = *(const float4*)(Mm + t * NT + s4);
+          x = fmaf(-m4.x, r[s4], x);
+          if (s4 + 1 < t) x = fmaf(-m4.y, r[s4 + 1], x);
+          if (s4 + 2 < t) x = fmaf(-m4.z, r[s4 + 2], x);
+          if (s4 + 3 < t) x = fmaf(-m4.w, r[s4 + 3], x);
         }
+        r[t] = x;
+      }
+      if (pub) {
+        float* Rj = (float*)(hl + kHR);
+#pragma unroll
+        for (int t = 0; t < NT; ++t) Rj[t * NT + l16] = (t < n && on) ? r[t] : 0.f;
       }
     }
     // everything is in LDS before the barrier
@@ -515,8 +574,10 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
   }
 
   // ================= row waves ====================================================
+  const int b = opaque_s(b0);
   constexpr int RPW = 16 * TPW;  // V-rows per wave
   constexpr int VB = TPW / 2;     // vblocks (32 rows) per wave
+  constexpr int VSTRIDE = RPW * ES + 16;  // LDS bytes per token of the wave's v rows
   const int wr = (w - U) - u * rpu;
   const int j = uni(wr / NWH), part = wr - j * NWH;  // value head in the unit, row block of it
   // (barrier 1: every chain wave's requests go first)
@@ -531,33 +592,39 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
   u32x4_t cw[TPW][2];
 #pragma unroll
   for (int i = 0; i < TPW; ++i) {
-    const uint32_t off = (uint32_t)(32 * (i >> 1) + 2 * l16 + (i & 1)) * ck_v + 16 * q4;
+    const uint32_t off = (uint32_t)(32 * (i >> 1) + 2 * l16 + (i & 1)) * ck_v + 32 * q4;
     cw[i][0] = *(g_u32x4*)(ck_rows + off);
-    cw[i][1] = *(g_u32x4*)(ck_rows + off + 64);
+    cw[i][1] = *(g_u32x4*)(ck_rows + off + 16);
   }
   GDNR_COMPILER_FENCE();
+  const StepArgs& A = opaque_args();
   int n, pos;
   bool do_flush;
-  read_meta(n, pos, do_flush);
-  uint8_t* scale_hv = a.scale + (bs * a.sc_b + hv * a.sc_h);
+  read_meta(A, n, pos, do_flush);
+  uint8_t* scale_hv = A.scale + (bs * A.sc_b + hv * A.sc_h);
   const int vb0 = R0 / kVBlock;
   float sct[VB];  // the vblock scales
 #pragma unroll
-  for (int p = 0; p < VB; ++p) sct[p] = f16_bits_to_f32(ld_u16_uniform(scale_hv + (vb0 + p) * a.sc_v));
-  // v rows of the filled slots: lane (nn, q4), token t = 4 q4 + e, rows
-  // (32 p + 2 nn, 32 p + 2 nn + 1) of vblock p; the new token's from
-  // mixed_qkv; slots at or past the fill re-read slot 0 (dropped below)
-  uint32_t vp[4][VB];
+  for (int p = 0; p < VB; ++p) sct[p] = f16_bits_to_f32(ld_u16_uniform(scale_hv + (vb0 + p) * A.sc_v));
+  // v rows of the filled slots in 16-byte pieces (CPT per token): load k of
+  // lane l is token vtok(k) = k TPL + l / CPT, bytes [16 (l % CPT), +16) of
+  // the wave's row block; the new token's from mixed_qkv; slots at or past
+  // the fill re-read slot 0 (dropped when used)
+  constexpr int CPT = RPW * ES / 16;  // pieces per token row block
+  constexpr int TPL = 64 / CPT;       // tokens per load
+  constexpr int NVL = NT / TPL;       // loads per lane
+  const int vpiece = lane % CPT;
+  auto vtok = [&](int k) { return k * TPL + lane / CPT; };
+  u32x4_t vq[NVL];
   {
-    const uint8_t* vbase = a.v + (bs * a.v_b + hv * a.v_h + (R0 + 2 * l16) * ES);
+    const uint8_t* vbase = A.v + (bs * A.v_b + hv * A.v_h + R0 * ES) + 16 * vpiece;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int t = 4 * q4 + e;
-      const uint8_t* src = vbase + (uint32_t)(t < n ? t : 0) * a.v_t;
+    for (int k = 0; k < NVL; ++k) {
+      const int t = vtok(k);
+      const uint8_t* src = vbase + (uint32_t)(t < n ? t : 0) * A.v_t;
       if constexpr (FUSED)
-        if (t == pos) src = a.mixed + (b * a.mx_b + (2 * a.H * K + hv * a.V + R0 + 2 * l16) * ES);
-#pragma unroll
-      for (int p = 0; p < VB; ++p) vp[e][p] = ld32(src + 64 * p);
+        if (t == pos) src = A.mixed + (b * A.mx_b + (2 * A.H * K + hv * A.V + R0) * ES) + 16 * vpiece;
+      vq[k] = *(g_u32x4*)src;
     }
   }
   GDNR_COMPILER_FENCE();
@@ -567,29 +634,36 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
   asm volatile("" ::: "memory");
 
   // ring append of the new token's v rows (full contract; this wave's rows,
-  // which no other wave reads): lanes of group q4 == pos / 4 hold them
+  // which no other wave reads): the lanes that loaded token pos
   if constexpr (FUSED) {
-    if (pos >= 0 && q4 == (pos >> 2)) {
-      const int e = pos & 3;
-      uint8_t* vw = a.v + (bs * a.v_b + (uint32_t)pos * a.v_t + hv * a.v_h + (R0 + 2 * l16) * ES);
+    if (pos >= 0) {
+      uint8_t* vw = A.v + (bs * A.v_b + (uint32_t)pos * A.v_t + hv * A.v_h + R0 * ES) + 16 * vpiece;
 #pragma unroll
-      for (int p = 0; p < VB; ++p)
-        *(uint32_t*)(vw + 64 * p) = e == 0 ? vp[0][p] : e == 1 ? vp[1][p] : e == 2 ? vp[2][p] : vp[3][p];
+      for (int k = 0; k < NVL; ++k)
+        if (vtok(k) == pos) *(u32x4_t*)vw = vq[k];
     }
   }
+  // the v rows go to LDS token-major ([16][VS] bytes; the replay once its
+  // products are issued, the flush first): lane (nn, q4) then reads the two
+  // rows of tiles (2p, 2p + 1) of token 4 q4 + e as one word
+  uint8_t* vl = ul + kUnitBase + wr * (NT * VSTRIDE);
+  auto stage_v = [&]() {
+#pragma unroll
+    for (int k = 0; k < NVL; ++k) *(u32x4_t*)(vl + vtok(k) * VSTRIDE + 16 * vpiece) = vq[k];
+  };
   // v of token 4 q4 + e for tile i (zero at or past the fill)
   auto vval = [&](int i, int e) {
-    const uint32_t wv = vp[e][i >> 1];
+    const uint32_t wv = *(const uint32_t*)(vl + (4 * q4 + e) * VSTRIDE + (32 * (i >> 1) + 2 * l16) * ES);
     const float x = act_val((i & 1) ? (wv >> 16) : wv);
     return (4 * q4 + e) < n ? x : 0.f;
   };
-  uint8_t* out_rows = a.out + (b * a.o_b + hv * a.o_h + R0 * ES);
+  uint8_t* out_rows = A.out + (b * A.o_b + hv * A.o_h + R0 * ES);
   // o of tiles 4 g .. 4 g + 3 from per-tile partials: lane (l16, q4) stores
   // the row of tile 4 g + q4
   auto store_out = [&](int g, float p0, float p1, float p2, float p3) {
     float o = rows_reduce_scatter(p0, p1, p2, p3);
     asm volatile("" : "+v"(o));  // (no tail shared between the branches)
-    Act::st(out_rows, 64 * g + 32 * (q4 >> 1) + 2 * l16 + (q4 & 1), o * a.out_scale);
+    Act::st(out_rows, 64 * g + 32 * (q4 >> 1) + 2 * l16 + (q4 & 1), o * A.out_scale);
   };
 
   if (!do_flush) {
@@ -597,47 +671,45 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
     // T_0 enters as the A operand rows 0 (hi), 1 (mid) and 2 (lo), the other
     // rows zero: lanes q4 == 0 get (S_0 T_0)[row] as the sum of their first
     // three outputs
-    const uint8_t* arow = hl + kHT0 + 256 * (l16 < 3 ? l16 : 0) + 32 * q4;
+    const uint8_t* arow = hl + kHT0 + 256 * (l16 < 3 ? l16 : 0) + 64 * q4;
     const float4 cc = *(const float4*)(hl + kHCoef + 16 * q4);
     const float t0s = ((const float*)(hl + kHLam))[1];
     // (the codes taken afresh: no conversion here is shared with the flush
     // branch, so none is hoisted above the branch)
 #pragma unroll
     for (int i = 0; i < TPW; ++i) asm volatile("" : "+v"(cw[i][0]), "+v"(cw[i][1]));
-    float part_[TPW];
+    // the products tile by tile as the codes land, then the v terms
+    float pt[TPW];
 #pragma unroll
     for (int i = 0; i < TPW; ++i) {
       f32x4_t c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int m = 0; m < 4; ++m) {
-        const u32x4_t x = *(const u32x4_t*)(arow + 128 * (m >> 1) + 16 * (m & 1));
+        const u32x4_t x = *(const u32x4_t*)(arow + 16 * m);
         c = mfma16(l16 < 3 ? x : u32x4_t{0u, 0u, 0u, 0u}, codes8(cw[i], m), c);
       }
+      pt[i] = (c[0] + (c[1] + c[2])) * (sct[i >> 1] * t0s);
+    }
+    stage_v();
+    float part_[TPW];
+#pragma unroll
+    for (int i = 0; i < TPW; ++i) {
       float wsum = cc.x * vval(i, 0);
       wsum = fmaf(cc.y, vval(i, 1), wsum);
       wsum = fmaf(cc.z, vval(i, 2), wsum);
       wsum = fmaf(cc.w, vval(i, 3), wsum);
-      part_[i] = fmaf(c[0] + (c[1] + c[2]), sct[i >> 1] * t0s, wsum);
+      part_[i] = pt[i] + wsum;
     }
 #pragma unroll
     for (int g = 0; g < TPW / 4; ++g) store_out(g, part_[4 * g], part_[4 * g + 1], part_[4 * g + 2], part_[4 * g + 3]);
     return;
   }
 
-  // registers are short in the flush: the v rows wait in LDS (read per tile)
-  uint8_t* vl = ul + kUnitBase + (wr * 64 + lane) * 16 * VB;
-#pragma unroll
-  for (int p = 0; p < VB; ++p) *(u32x4_t*)(vl + 16 * p) = u32x4_t{vp[0][p], vp[1][p], vp[2][p], vp[3][p]};
-  asm volatile("" ::: "memory");
-  auto vval_l = [&](int i, int e) {
-    const uint32_t wv = *(const uint32_t*)(vl + 16 * (i >> 1) + 4 * e);
-    const float x = act_val((i & 1) ? (wv >> 16) : wv);
-    return (4 * q4 + e) < n ? x : 0.f;
-  };
   // ---- flush, one vblock (tiles 2p, 2p + 1) at a time: P = X S_0^T of its
   // rows on every ring token, W = v - pre P, U = R W, U~ = post U, then
   // S_n = lam S_0 + K^T U~ by 16 x 4 column groups in two passes: the vblock
   // amax and o = S_n q, then the requantisation in place
+  stage_v();
   const float lam = ((const float*)(hl + kHLam))[0];
   float opart[TPW];
   // S_n column group ct of tile i: lane (nn, q4) gets
@@ -683,7 +755,7 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
 #pragma unroll
       for (int m = 0; m < 4; ++m) {
         const u32x4_t x =
-            *(const u32x4_t*)(ul + kLX + l16 * kXStride + 128 * (m >> 1) + 16 * (m & 1) + 32 * q4);
+            *(const u32x4_t*)(ul + kLX + l16 * kXStride + 64 * q4 + 16 * m);
         pr = mfma16(x, codes8(cw[i], m), pr);
       }
       float wv[4], post[4];
@@ -692,7 +764,7 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
         const int t = 4 * q4 + e;
         const float2 fc = *(const float2*)(hl + kHFac + 16 * t);
         post[e] = fc.y;
-        wv[e] = t < n ? vval_l(i, e) - fc.x * (pr[e] * sct[p]) : 0.f;
+        wv[e] = t < n ? vval(i, e) - fc.x * (pr[e] * sct[p]) : 0.f;
       }
       const float4 rr = *(const float4*)(hl + kHR + 4 * (l16 * NT + 4 * q4));
       const float rrv[4] = {rr.x, rr.y, rr.z, rr.w};
@@ -734,7 +806,7 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
       const u32x4_t a_ls = a_ls_of(p);
 #pragma unroll
       for (int ct = 0; ct < 8; ++ct) {
-        const uint2 qb = *(const uint2*)(ul + kLQK + 128 * (ct >> 2) + 32 * q4 + 8 * (ct & 3));
+        const uint2 qb = *(const uint2*)(ul + kLQK + 64 * q4 + 8 * ct);
         const float2 qa = Act::from_pair(qb.x), qc = Act::from_pair(qb.y);
         const f32x4_t s0 = s_group(2 * p, ct, a_ls, packed[0]);
         const f32x4_t s1 = s_group(2 * p + 1, ct, a_ls, packed[1]);
@@ -774,13 +846,13 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
 #pragma unroll
       for (int ii = 0; ii < 2; ++ii) {
         const int i = 2 * p + ii;
-        const uint32_t ro = (uint32_t)(32 * p + 2 * l16 + ii) * ck_v + 16 * q4;
+        const uint32_t ro = (uint32_t)(32 * p + 2 * l16 + ii) * ck_v + 32 * q4;
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
           uint32_t wd[4];
 #pragma unroll
           for (int w4 = 0; w4 < 4; ++w4) wd[w4] = quant(s_group(i, 4 * hh + w4, a_ls, packed[ii]));
-          *(g_u32x4_w*)(ck_rows + ro + 64 * hh) = u32x4_t{wd[0], wd[1], wd[2], wd[3]};
+          *(g_u32x4_w*)(ck_rows + ro + 16 * hh) = u32x4_t{wd[0], wd[1], wd[2], wd[3]};
           __builtin_amdgcn_sched_barrier(0);
         }
       }
@@ -805,7 +877,7 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
         return wd;
       });
     }
-    if (lane == 0) *(uint16_t*)(scale_hv + (vb0 + p) * a.sc_v) = __builtin_bit_cast(uint16_t, (_Float16)s32);
+    if (lane == 0) *(uint16_t*)(scale_hv + (vb0 + p) * A.sc_v) = __builtin_bit_cast(uint16_t, (_Float16)s32);
   }
 #pragma unroll
   for (int g = 0; g < TPW / 4; ++g) store_out(g, opart[4 * g], opart[4 * g + 1], opart[4 * g + 2], opart[4 * g + 3]);
