@@ -440,11 +440,15 @@ void fit_decode(gdnr::ReplayArgs* a) {
   a->gw = a->G % 2 == 0 ? 2 : 1;  // value heads per unit (at most 2; they share the unit's chain wave)
   a->sw = a->V / 64;
   // units per workgroup: as many as fit one CU (12 waves) while the grid
-  // still covers every CU, dividing the units of a sequence
+  // still covers every CU; the kernel takes a workgroup's units as SP
+  // sequences x HP head groups (4 = 2 x 2, 2 = 2 x 1), which must divide B
+  // and the head groups of a sequence
   const int32_t per_seq = a->H * (a->G / a->gw), waves = 1 + a->gw * nwh;
   a->units = 1;
   for (int32_t u : {4, 2}) {
-    if (per_seq % u == 0 && u * waves <= 12 && (int64_t)a->B * per_seq / u >= gdnr::device_cus()) {
+    const int32_t hp = u == 4 ? 2 : 1, sp = u / hp;
+    if (a->B % sp == 0 && per_seq % hp == 0 && u * waves <= 12 &&
+        (int64_t)a->B * per_seq / u >= gdnr::device_cus()) {
       a->units = u;
       break;
     }

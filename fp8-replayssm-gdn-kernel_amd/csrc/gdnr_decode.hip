@@ -260,9 +260,14 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
   // (uniform indices: the divisions are VALU code, readfirstlane keeps the
   // results and every address built from them in SGPRs)
   const int u = uni(chain ? w : (w - U) / rpu);  // the wave's unit
-  const int r = (int)blockIdx.x * U + u;         // unit within the sequence: (key head, group)
+  // the U units of a workgroup: SP consecutive sequences x HP consecutive
+  // (key head, value-head group) pairs; a flushing sequence's heads spread
+  // over several workgroups, a workgroup's codes over few rows of memory
+  const int HP = U == 4 ? 2 : 1, SP = U == 4 ? 2 : U;
+  const int uh = HP == 2 ? (u & 1) : 0, us = HP == 2 ? (u >> 1) : u;
+  const int r = uni((int)blockIdx.x * HP + uh);  // the unit's (key head, value-head group)
   const int n_grp = uni(G / gw);
-  const int h = uni(r / n_grp), grp = r - h * n_grp, b0 = blockIdx.y;
+  const int h = uni(r / n_grp), grp = r - h * n_grp, b0 = uni((int)blockIdx.y * SP + us);
   const int hv0 = h * G + grp * gw;              // first value head of the unit
   uint8_t* const ul = lds + u * unit_lds(rpu, TPW / 2);  // the unit's LDS block
 
@@ -707,19 +712,19 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
 
   // ---- flush, one vblock (tiles 2p, 2p + 1) at a time: P = X S_0^T of its
   // rows on every ring token, W = v - pre P, U = R W, U~ = post U, then
-  // S_n = lam S_0 + K^T U~ by 16 x 4 column groups in two passes: the vblock
-  // amax and o = S_n q, then the requantisation in place
+  // S_n = lam S_0 + K^T U~ by 16 x 4 column groups, kept in registers: the
+  // vblock amax and o = S_n q as the groups complete, then the
+  // requantisation in place. The codes of vblock p + 1 are read again
+  // (prefetched while p is rebuilt) rather than held since the stream.
   stage_v();
   const float lam = ((const float*)(hl + kHLam))[0];
-  float opart[TPW];
   // S_n column group ct of tile i: lane (nn, q4) gets
-  // S_n[row r(i, nn)][64 (ct / 4) + 16 q4 + 4 (ct % 4) + e], byte 4 (ct % 4) + e
-  // of its code chunk ct / 4. lam S_0 enters through the MFMA as
-  // (ls I) S_0^T with ls = lam * scale split into hi + lo halves; each hi/lo
-  // pair is one 16x16x32 MFMA (k-slots 8 q4 + j: j < 4 the hi part, j >= 4
-  // the lo part of token / column 4 q4 + (j & 3)).
-  auto a_ls_of = [&](int p) {
-    const float ls = lam * sct[p];
+  // S_n[row r(i, nn)][32 q4 + 4 ct + e], code byte 4 ct + e of its 32. lam
+  // S_0 enters through the MFMA as (ls I) S_0^T with ls = lam * scale split
+  // into hi + lo halves; each hi/lo pair is one 16x16x32 MFMA (k-slots
+  // 8 q4 + j: j < 4 the hi part, j >= 4 the lo part of column 4 q4 + (j & 3)).
+  auto a_ls_of = [&](float scp) {
+    const float ls = lam * scp;
     uint32_t hb, lb;
     if constexpr (kBF16) {
       hb = f32_to_bf16(ls);
@@ -734,46 +739,59 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
     const uint32_t h2 = hb | (hb << 16), l2 = lb | (lb << 16);
     return u32x4_t{h2 & (d0 | d1), h2 & (d2 | d3), l2 & (d0 | d1), l2 & (d2 | d3)};
   };
-  auto s_group = [&](int i, int ct, const u32x4_t& a_ls, const u32x4_t& pk) {
-    uint32_t cword = cw[i][ct >> 2][ct & 3];
-    asm volatile("" : "+v"(cword));  // converted again at every use (no register kept)
-    const uint2 c2 = codes4(cword);
-    const f32x4_t z = {0.f, 0.f, 0.f, 0.f};
-    const f32x4_t s0 = mfma16(a_ls, u32x4_t{c2.x, c2.y, c2.x, c2.y}, z);
-    int ko = kLKT + 2 * ((ct * 16 + l16) * 16 + 4 * q4);
-    asm volatile("" : "+v"(ko));  // read again at every use (no register kept)
-    const uint2 k2 = *(const uint2*)(ul + ko);
-    return mfma16(u32x4_t{k2.x, k2.y, k2.x, k2.y}, pk, s0);
-  };
+  u32x4_t cur[2][2] = {{cw[0][0], cw[0][1]}, {cw[1][0], cw[1][1]}};
+  const uint8_t* rows_again = opaque_uniform(ck_rows);
+  // (a loop, not unrolled: one vblock's registers at a time; the indices
+  // that depend on p are formed by selects, not by indexing registers)
+  float opart_all[TPW];
 #pragma unroll
+  for (int i = 0; i < TPW; ++i) opart_all[i] = 0.f;
+#pragma unroll 1
   for (int p = 0; p < VB; ++p) {
+    float scp = sct[0];
+#pragma unroll
+    for (int q = 1; q < VB; ++q) scp = p == q ? sct[q] : scp;
     u32x4_t packed[2];
 #pragma unroll
     for (int ii = 0; ii < 2; ++ii) {
       const int i = 2 * p + ii;
-      f32x4_t pr = {0.f, 0.f, 0.f, 0.f};
+      // P on the ring tokens, and on the query as a block of its own (row 0)
+      f32x4_t pr = {0.f, 0.f, 0.f, 0.f}, pq = pr;
+      int xo = kLX + l16 * kXStride + 64 * q4, qo = kLQK + 64 * q4;
+      asm volatile("" : "+v"(xo), "+v"(qo));  // read in the loop, not held across it
 #pragma unroll
       for (int m = 0; m < 4; ++m) {
-        const u32x4_t x =
-            *(const u32x4_t*)(ul + kLX + l16 * kXStride + 64 * q4 + 16 * m);
-        pr = mfma16(x, codes8(cw[i], m), pr);
+        const u32x4_t x = *(const u32x4_t*)(ul + xo + 16 * m);
+        const u32x4_t qx = *(const u32x4_t*)(ul + qo + 16 * m);
+        const u32x4_t bv = codes8(cur[ii], m);
+        pr = mfma16(x, bv, pr);
+        pq = mfma16(l16 == 0 ? qx : u32x4_t{0u, 0u, 0u, 0u}, bv, pq);
       }
-      float wv[4], post[4];
+      float wv[4], post[4], dqt[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int t = 4 * q4 + e;
-        const float2 fc = *(const float2*)(hl + kHFac + 16 * t);
+        const float4 fc = *(const float4*)(hl + kHFac + 16 * t);
         post[e] = fc.y;
-        wv[e] = t < n ? vval(i, e) - fc.x * (pr[e] * sct[p]) : 0.f;
+        dqt[e] = fc.z;
+        const float vv = vval(i, e);
+        wv[e] = t < n ? vv - fc.x * (pr[e] * scp) : 0.f;
       }
       const float4 rr = *(const float4*)(hl + kHR + 4 * (l16 * NT + 4 * q4));
       const float rrv[4] = {rr.x, rr.y, rr.z, rr.w};
       f32x4_t u = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int e = 0; e < 4; ++e) u = __builtin_amdgcn_mfma_f32_16x16x4f32(rrv[e], wv[e], u, 0, 0, 0);
+      // o = S_n q = lam (S_0 q) + sum_t U~_t (k_t . q): this lane's share
       float ut[4];
+      float op = (lam * scp) * pq[0];  // (zero at lanes q4 != 0)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) ut[e] = u[e] * post[e];
+      for (int e = 0; e < 4; ++e) {
+        ut[e] = u[e] * post[e];
+        op = fmaf(ut[e], dqt[e], op);
+      }
+#pragma unroll
+      for (int k = 0; k < TPW; ++k) opart_all[k] = k == i ? op : opart_all[k];
       if constexpr (kBF16) {
         // hi/lo split: U~ = hi + lo to ~16 bits, both halves bf16 operands
         const uint32_t h01 = pack_bf16x2(ut[0], ut[1]), h23 = pack_bf16x2(ut[2], ut[3]);
@@ -794,43 +812,47 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
         };
         packed[ii] = u32x4_t{pk(hh[0], hh[1]), pk(hh[2], hh[3]), pk(ll[0], ll[1]), pk(ll[2], ll[3])};
       }
-      // one tile at a time (the second tile's products are not issued ahead)
-      asm volatile("" : "+v"(packed[ii]));
-      __builtin_amdgcn_sched_barrier(0);
     }
-    // pass 1: the vblock amax (|x| max, NaN propagating like torch.amax) and
-    // the output partials o = S_n q over the lane's columns
+    // pass 1: S_n of the vblock's 2 x 8 column groups (kept) and the vblock
+    // amax (|x| max, NaN propagating like torch.amax)
+    f32x4_t sv[2][8];
     float am = 0.f;
-    float op0 = 0.f, op1 = 0.f;
     {
-      const u32x4_t a_ls = a_ls_of(p);
+      const u32x4_t a_ls = a_ls_of(scp);
 #pragma unroll
       for (int ct = 0; ct < 8; ++ct) {
-        const uint2 qb = *(const uint2*)(ul + kLQK + 64 * q4 + 8 * ct);
-        const float2 qa = Act::from_pair(qb.x), qc = Act::from_pair(qb.y);
-        const f32x4_t s0 = s_group(2 * p, ct, a_ls, packed[0]);
-        const f32x4_t s1 = s_group(2 * p + 1, ct, a_ls, packed[1]);
-        am = __builtin_elementwise_maximum(am, __builtin_elementwise_maximum(__builtin_fabsf(s0[0]), __builtin_fabsf(s0[1])));
-        am = __builtin_elementwise_maximum(am, __builtin_elementwise_maximum(__builtin_fabsf(s0[2]), __builtin_fabsf(s0[3])));
-        am = __builtin_elementwise_maximum(am, __builtin_elementwise_maximum(__builtin_fabsf(s1[0]), __builtin_fabsf(s1[1])));
-        am = __builtin_elementwise_maximum(am, __builtin_elementwise_maximum(__builtin_fabsf(s1[2]), __builtin_fabsf(s1[3])));
-        op0 = fmaf(s0[0], qa.x, op0);
-        op0 = fmaf(s0[1], qa.y, op0);
-        op0 = fmaf(s0[2], qc.x, op0);
-        op0 = fmaf(s0[3], qc.y, op0);
-        op1 = fmaf(s1[0], qa.x, op1);
-        op1 = fmaf(s1[1], qa.y, op1);
-        op1 = fmaf(s1[2], qc.x, op1);
-        op1 = fmaf(s1[3], qc.y, op1);
-        // one column group at a time: the products of later groups are not
-        // issued ahead (each would hold four more registers)
+#pragma unroll
+        for (int ii = 0; ii < 2; ++ii) {
+          const uint2 c2 = codes4(cur[ii][ct >> 2][ct & 3]);
+          const f32x4_t z = {0.f, 0.f, 0.f, 0.f};
+          const f32x4_t s0 = mfma16(a_ls, u32x4_t{c2.x, c2.y, c2.x, c2.y}, z);
+          const uint2 k2 = *(const uint2*)(ul + kLKT + 2 * ((ct * 16 + l16) * 16 + 4 * q4));
+          sv[ii][ct] = mfma16(u32x4_t{k2.x, k2.y, k2.x, k2.y}, packed[ii], s0);
+        }
+        // (a group's first product completes into its second before the
+        // next group starts: no more than one intermediate is held)
         __builtin_amdgcn_sched_barrier(0);
       }
+#pragma unroll
+      for (int ct = 0; ct < 8; ++ct) {
+#pragma unroll
+        for (int ii = 0; ii < 2; ++ii) {
+          const f32x4_t sg = sv[ii][ct];
+          am = __builtin_elementwise_maximum(am, __builtin_elementwise_maximum(__builtin_fabsf(sg[0]), __builtin_fabsf(sg[1])));
+          am = __builtin_elementwise_maximum(am, __builtin_elementwise_maximum(__builtin_fabsf(sg[2]), __builtin_fabsf(sg[3])));
+        }
+      }
     }
-    // computed here, not sunk to the output: their inputs die here
-    asm volatile("" : "+v"(op0), "+v"(op1));
-    opart[2 * p] = op0;
-    opart[2 * p + 1] = op1;
+    // the next vblock's codes, read (into the same registers) while this
+    // one is requantised
+    if (p + 1 < VB) {
+#pragma unroll
+      for (int ii = 0; ii < 2; ++ii) {
+        const uint32_t off = (uint32_t)(32 * (p + 1) + 2 * l16 + ii) * ck_v + 32 * q4;
+        cur[ii][0] = *(g_u32x4*)(rows_again + off);
+        cur[ii][1] = *(g_u32x4*)(rows_again + off + 16);
+      }
+    }
     const uint32_t amb = wave_max_u32(__float_as_uint(am));
     // the reference quantiser (ref:36-37,83-99): s = amax / 448 (1 when amax
     // is not > 0); codes = e4m3fn(clamp(x / s, +-448)) with the unrounded s;
@@ -839,21 +861,18 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
     const float s32 = (amax > 0.0f) ? amax / 448.0f : 1.0f;
     const bool fast = quotient_fast(amb, s32);
     const float rcp = 1.0f / s32;
-    // pass 2: the same column groups again, requantised and stored (the
-    // division path of non-finite or tiny-scale blocks is a loop of its own)
+    // pass 2: the kept column groups requantised and stored (the division
+    // path of non-finite or tiny-scale blocks is a loop of its own)
     auto pass2 = [&](auto quant) {
-      const u32x4_t a_ls = a_ls_of(p);
 #pragma unroll
       for (int ii = 0; ii < 2; ++ii) {
-        const int i = 2 * p + ii;
         const uint32_t ro = (uint32_t)(32 * p + 2 * l16 + ii) * ck_v + 32 * q4;
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
           uint32_t wd[4];
 #pragma unroll
-          for (int w4 = 0; w4 < 4; ++w4) wd[w4] = quant(s_group(i, 4 * hh + w4, a_ls, packed[ii]));
+          for (int w4 = 0; w4 < 4; ++w4) wd[w4] = quant(sv[ii][4 * hh + w4]);
           *(g_u32x4_w*)(ck_rows + ro + 16 * hh) = u32x4_t{wd[0], wd[1], wd[2], wd[3]};
-          __builtin_amdgcn_sched_barrier(0);
         }
       }
     };
@@ -880,12 +899,14 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
     if (lane == 0) *(uint16_t*)(scale_hv + (vb0 + p) * A.sc_v) = __builtin_bit_cast(uint16_t, (_Float16)s32);
   }
 #pragma unroll
-  for (int g = 0; g < TPW / 4; ++g) store_out(g, opart[4 * g], opart[4 * g + 1], opart[4 * g + 2], opart[4 * g + 3]);
+  for (int g = 0; g < TPW / 4; ++g)
+    store_out(g, opart_all[4 * g], opart_all[4 * g + 1], opart_all[4 * g + 2], opart_all[4 * g + 3]);
 }
 
 template <int TPW, int NWH, bool FUSED, bool GATE_F32, bool SLOTS>
 int launch_variant(const StepArgs& a, hipStream_t s) {
-  const dim3 grid((unsigned)(a.H * (a.G / a.gw) / a.units), (unsigned)a.B),
+  const int hp = a.units == 4 ? 2 : 1, sp = a.units / hp;  // as in the kernel
+  const dim3 grid((unsigned)(a.H * (a.G / a.gw) / hp), (unsigned)(a.B / sp)),
       block((unsigned)(64 * a.units * (1 + a.gw * NWH)));
   auto kernel = decode_kernel<TPW, NWH, FUSED, GATE_F32, SLOTS>;
   if (a.lds_bytes > 64 * 1024) {

@@ -36,8 +36,12 @@ ACTS = ("bf16", "f16", "f32")  # activation dtypes, one kernel object each (GDNR
 KERNEL_SOURCES = ("gdnr_kernels", "gdnr_step", "gdnr_decode")  # compiled once per activation dtype
 SINGLE_SOURCES = ("gdnr_rmw", "gdnr_formats", "gdnr_status")  # compiled once (dtypes are template arguments)
 # per-source device flags: the decode kernel's first 13 argument dwords are
-# preloaded into SGPRs at wave launch (gfx950 kernarg preload)
-SOURCE_FLAGS = {"gdnr_decode": ["-mllvm", "-amdgpu-kernarg-preload-count=13"]}
+# preloaded into SGPRs at wave launch (gfx950 kernarg preload), and its
+# wave-uniform branches (workgroup role, replay or flush) are left as scalar
+# branches rather than structurised into a chain in which one arm's values
+# stay live across the other
+SOURCE_FLAGS = {"gdnr_decode": ["-mllvm", "-amdgpu-kernarg-preload-count=13",
+                                "-mllvm", "-structurizecfg-skip-uniform-regions=true"]}
 
 
 def _run(cmd: list[str], verbose: bool) -> None:
