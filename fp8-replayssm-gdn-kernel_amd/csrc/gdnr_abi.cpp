@@ -637,35 +637,15 @@ int gdnr_replay_fp8(const gdnr_tensor* checkpoint, const gdnr_tensor* checkpoint
   return hip_status(launch_replay(a, g.act, gdnr::kModeReplay, false, stream));
 }
 
-int gdnr_replay_fp8_split(const gdnr_tensor* checkpoint, const gdnr_tensor* checkpoint_scale, const gdnr_tensor* q,
-                          const gdnr_tensor* k_cache, const gdnr_tensor* v_cache, const gdnr_tensor* g_cache,
-                          const gdnr_tensor* beta_cache, const gdnr_tensor* valid_len,
-                          const gdnr_tensor* transformed_query, const gdnr_tensor* coefficient,
-                          const gdnr_tensor* out, int32_t block_v, int32_t block_kc, int32_t precompute_grouped,
-                          void* stream) {
-  g_last_error.clear();
-  Geometry g;
-  GDNR_TRY(check_ring(k_cache, v_cache, g_cache, beta_cache, &g, 16));
-  GDNR_TRY(check_checkpoint(checkpoint, checkpoint_scale, g));
-  GDNR_TRY(check_act_tensor(q, "q", 3, {g.B, g.H, g.K}, g.act, 16));
-  GDNR_TRY(check_index_vec(valid_len, "valid_len", g.B, false));
-  GDNR_TRY(check_desc(transformed_query, "transformed_query_buffer", 3));
-  GDNR_TRY(check_dtype(transformed_query, "transformed_query_buffer", {GDNR_DTYPE_F32}));
-  GDNR_TRY(check_shape(transformed_query, "transformed_query_buffer", {g.B, g.HV, g.K}));
-  GDNR_TRY(check_inner_unit(transformed_query, "transformed_query_buffer"));
-  GDNR_TRY(check_align(transformed_query, "transformed_query_buffer", 16));
-  GDNR_TRY(check_desc(coefficient, "coefficient_buffer", 3));
-  GDNR_TRY(check_dtype(coefficient, "coefficient_buffer", {GDNR_DTYPE_F32}));
-  GDNR_TRY(check_shape(coefficient, "coefficient_buffer", {g.B, g.HV}));
-  if (coefficient->shape[2] < g.L)
-    return fail(GDNR_ERR_INVALID_ARGUMENT, "coefficient_buffer: last dim %lld is shorter than the ring (%lld)",
-                (long long)coefficient->shape[2], (long long)g.L);
-  GDNR_TRY(check_act_tensor(out, "out", 3, {g.B, g.HV, g.V}, g.act, 2));
-  GDNR_TRY(check_block_v(block_v, g));
-  if (block_kc != 128 && block_kc != g.K)
-    return fail(GDNR_ERR_UNSUPPORTED, "block_kc=%d: the checkpoint is streamed in whole 128-column rows", block_kc);
-  if (g.B == 0) return GDNR_OK;
-
+namespace {
+// The two launches of the split replay (precompute, then apply) once the
+// arguments are validated; tq [B,HV,K] and coef [B,HV,>=L] f32 with element
+// strides.
+int split_launch(const Geometry& g, const gdnr_tensor* checkpoint, const gdnr_tensor* checkpoint_scale,
+                 const gdnr_tensor* q, const gdnr_tensor* k_cache, const gdnr_tensor* v_cache,
+                 const gdnr_tensor* g_cache, const gdnr_tensor* beta_cache, const gdnr_tensor* valid_len,
+                 float* tq, int64_t tq_b, int64_t tq_h, float* coef, int64_t co_b, int64_t co_h, int64_t co_t,
+                 const gdnr_tensor* out, int32_t block_v, int32_t precompute_grouped, void* stream) {
   gdnr::ReplayArgs a = {};
   fill_common(&a, g, block_v);
   fill_ckpt(&a, checkpoint, checkpoint_scale);
@@ -675,13 +655,13 @@ int gdnr_replay_fp8_split(const gdnr_tensor* checkpoint, const gdnr_tensor* chec
   a.q_h = q->strides[1];
   fill_index(valid_len, &a.valid_len, &a.vl_s);
   a.flush = nullptr;
-  a.tq = (float*)transformed_query->data;
-  a.tq_b = transformed_query->strides[0];
-  a.tq_h = transformed_query->strides[1];
-  a.coef = (float*)coefficient->data;
-  a.co_b = coefficient->strides[0];
-  a.co_h = coefficient->strides[1];
-  a.co_t = coefficient->strides[2];
+  a.tq = tq;
+  a.tq_b = tq_b;
+  a.tq_h = tq_h;
+  a.coef = coef;
+  a.co_b = co_b;
+  a.co_h = co_h;
+  a.co_t = co_t;
   a.out = out->data;
   a.o_b = out->strides[0];
   a.o_h = out->strides[1];
@@ -699,6 +679,77 @@ int gdnr_replay_fp8_split(const gdnr_tensor* checkpoint, const gdnr_tensor* chec
   GDNR_TRY(hip_status(launch_precompute(pre, g.act, stream)));
   GDNR_TRY(fit_lds(&a, elem_size(g.act), false, true));
   return hip_status(launch_replay(a, g.act, gdnr::kModeApply, false, stream));
+}
+
+// argument checks shared by the two split entry points (all but the buffers)
+int check_split(const gdnr_tensor* checkpoint, const gdnr_tensor* checkpoint_scale, const gdnr_tensor* q,
+                const gdnr_tensor* k_cache, const gdnr_tensor* v_cache, const gdnr_tensor* g_cache,
+                const gdnr_tensor* beta_cache, const gdnr_tensor* valid_len, const gdnr_tensor* out,
+                int32_t block_v, int32_t block_kc, Geometry* g) {
+  GDNR_TRY(check_ring(k_cache, v_cache, g_cache, beta_cache, g, 16));
+  GDNR_TRY(check_checkpoint(checkpoint, checkpoint_scale, *g));
+  GDNR_TRY(check_act_tensor(q, "q", 3, {g->B, g->H, g->K}, g->act, 16));
+  GDNR_TRY(check_index_vec(valid_len, "valid_len", g->B, false));
+  GDNR_TRY(check_act_tensor(out, "out", 3, {g->B, g->HV, g->V}, g->act, 2));
+  GDNR_TRY(check_block_v(block_v, *g));
+  if (block_kc != 128 && block_kc != g->K)
+    return fail(GDNR_ERR_UNSUPPORTED, "block_kc=%d: the checkpoint is streamed in whole 128-column rows", block_kc);
+  return GDNR_OK;
+}
+}  // namespace
+
+int gdnr_replay_fp8_split(const gdnr_tensor* checkpoint, const gdnr_tensor* checkpoint_scale, const gdnr_tensor* q,
+                          const gdnr_tensor* k_cache, const gdnr_tensor* v_cache, const gdnr_tensor* g_cache,
+                          const gdnr_tensor* beta_cache, const gdnr_tensor* valid_len,
+                          const gdnr_tensor* transformed_query, const gdnr_tensor* coefficient,
+                          const gdnr_tensor* out, int32_t block_v, int32_t block_kc, int32_t precompute_grouped,
+                          void* stream) {
+  g_last_error.clear();
+  Geometry g;
+  GDNR_TRY(check_split(checkpoint, checkpoint_scale, q, k_cache, v_cache, g_cache, beta_cache, valid_len, out,
+                       block_v, block_kc, &g));
+  GDNR_TRY(check_desc(transformed_query, "transformed_query_buffer", 3));
+  GDNR_TRY(check_dtype(transformed_query, "transformed_query_buffer", {GDNR_DTYPE_F32}));
+  GDNR_TRY(check_shape(transformed_query, "transformed_query_buffer", {g.B, g.HV, g.K}));
+  GDNR_TRY(check_inner_unit(transformed_query, "transformed_query_buffer"));
+  GDNR_TRY(check_align(transformed_query, "transformed_query_buffer", 16));
+  GDNR_TRY(check_desc(coefficient, "coefficient_buffer", 3));
+  GDNR_TRY(check_dtype(coefficient, "coefficient_buffer", {GDNR_DTYPE_F32}));
+  GDNR_TRY(check_shape(coefficient, "coefficient_buffer", {g.B, g.HV}));
+  if (coefficient->shape[2] < g.L)
+    return fail(GDNR_ERR_INVALID_ARGUMENT, "coefficient_buffer: last dim %lld is shorter than the ring (%lld)",
+                (long long)coefficient->shape[2], (long long)g.L);
+  if (g.B == 0) return GDNR_OK;
+  return split_launch(g, checkpoint, checkpoint_scale, q, k_cache, v_cache, g_cache, beta_cache, valid_len,
+                      (float*)transformed_query->data, transformed_query->strides[0], transformed_query->strides[1],
+                      (float*)coefficient->data, coefficient->strides[0], coefficient->strides[1],
+                      coefficient->strides[2], out, block_v, precompute_grouped, stream);
+}
+
+int gdnr_replay_fp8_split_noalloc(const gdnr_tensor* checkpoint, const gdnr_tensor* checkpoint_scale,
+                                  const gdnr_tensor* q, const gdnr_tensor* k_cache, const gdnr_tensor* v_cache,
+                                  const gdnr_tensor* g_cache, const gdnr_tensor* beta_cache,
+                                  const gdnr_tensor* valid_len, const gdnr_tensor* out, int32_t block_v,
+                                  int32_t block_kc, int32_t precompute_grouped, void* stream) {
+  g_last_error.clear();
+  Geometry g;
+  GDNR_TRY(check_split(checkpoint, checkpoint_scale, q, k_cache, v_cache, g_cache, beta_cache, valid_len, out,
+                       block_v, block_kc, &g));
+  // T_0 [B,HV,K] then the coefficients [B,HV,L], packed, in the device array
+  const int64_t heads = (int64_t)g.B * g.HV;
+  const int64_t tq_bytes = heads * g.K * 4, bytes = tq_bytes + heads * g.L * 4;
+  if (bytes > (int64_t)gdnr::kSplitScratchBytes)
+    return fail(GDNR_ERR_UNSUPPORTED,
+                "split scratch: B*HV=%lld with K=%lld and ring length %lld needs %lld bytes, more than the %lld "
+                "this entry point holds per GPU (use gdnr_replay_fp8_split with caller buffers)",
+                (long long)heads, (long long)g.K, (long long)g.L, (long long)bytes,
+                (long long)gdnr::kSplitScratchBytes);
+  if (g.B == 0) return GDNR_OK;
+  uint8_t* scratch = gdnr::split_scratch();
+  if (!scratch) return fail(GDNR_ERR_HIP, "split scratch: hipGetSymbolAddress failed on the current device");
+  return split_launch(g, checkpoint, checkpoint_scale, q, k_cache, v_cache, g_cache, beta_cache, valid_len,
+                      (float*)scratch, (int64_t)g.HV * g.K, g.K, (float*)(scratch + tq_bytes), (int64_t)g.HV * g.L,
+                      g.L, 1, out, block_v, precompute_grouped, stream);
 }
 
 int gdnr_prep_ring(const gdnr_tensor* mixed_qkv, const gdnr_tensor* a, const gdnr_tensor* b,

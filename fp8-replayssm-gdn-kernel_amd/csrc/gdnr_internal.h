@@ -177,6 +177,12 @@ int32_t decode_lds_bytes(int32_t units, int32_t row_waves, int32_t vblocks);
 uint32_t* status_word();
 int read_status(uint32_t* count, bool reset);
 int device_cus();
+// The split replay's device array for gdnr_replay_fp8_split_noalloc (T_0 and
+// the coefficients, packed; 3 MiB per GPU: B*HV <= 4096 at K = 128 with a
+// ring of up to 64), and its address on the current device (nullptr if the
+// symbol cannot be resolved).
+constexpr int64_t kSplitScratchBytes = 3 << 20;
+uint8_t* split_scratch();
 int launch_quantize(const QuantArgs& a, void* stream);
 int launch_rmw_step(const RmwArgs& a, int state_dt, int act_dt, void* stream);
 int launch_rmw_packed(const RmwArgs& a, int state_dt, int act_dt, bool gate_f32, void* stream);

@@ -1,5 +1,7 @@
 // gdnr_status.hip -- the device word through which kernels report bounded
-// waits that gave up (an LDS flag never raised), and its host read-out.
+// waits that gave up (an LDS flag never raised), and its host read-out; the
+// device array of the split replay entry point that allocates nothing; the
+// compute-unit count of the current device.
 //
 // One word per device (a file-scope __device__ variable: every GPU that
 // loads the library holds its own copy). Kernels add to it with a global
@@ -36,6 +38,24 @@ int read_status(uint32_t* count, bool reset) {
   if (e == hipSuccess && reset) e = hipMemset(p, 0, sizeof(uint32_t));
   if (e == hipSuccess) e = hipDeviceSynchronize();
   return (int)e;
+}
+
+// The split replay's scratch for the entry point that allocates nothing. One
+// array per GPU for the life of the process; host code reaches it through
+// the address hipGetSymbolAddress returns on that GPU, never through the
+// array's name (a host-side stand-in).
+static __device__ __align__(256) uint8_t scratch[kSplitScratchBytes];
+static uint8_t* g_scratch_ptr[kMaxDevices] = {};
+
+uint8_t* split_scratch() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess) return nullptr;
+    g_scratch_ptr[dev] = (uint8_t*)p;  // the same address on every call: a benign race between threads
+  }
+  return g_scratch_ptr[dev];
 }
 
 // compute units of the current device (cached per device; 256 if the query fails)

@@ -60,6 +60,7 @@ class GdnrTensor(ctypes.Structure):
 ENTRY_POINTS = {
     "gdnr_replay_fp8": (10, 1),
     "gdnr_replay_fp8_split": (11, 3),
+    "gdnr_replay_fp8_split_noalloc": (9, 3),
     "gdnr_prep_ring": (11, 1),
     "gdnr_prep_replay_fp8": (16, 1),
     "gdnr_prep_replay_fp8_slots": (17, 1),

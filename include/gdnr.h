@@ -135,6 +135,25 @@ int gdnr_replay_fp8_split(const gdnr_tensor* checkpoint, const gdnr_tensor* chec
                           void* stream);
 
 /*
+ * gdnr_replay_fp8_split without the two buffers: T_0 and the coefficients
+ * live in a device array of the library (3 MiB per GPU, held until the
+ * process ends), so the call allocates nothing. No counterpart in the
+ * reference: it is for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). Limit:
+ * B*HV*(K + ring length)*4 bytes <= 3 MiB (B*HV <= 4096 at K = 128 with a
+ * ring of up to 64); larger calls return GDNR_ERR_UNSUPPORTED. Every call on
+ * a GPU shares that GPU's array: calls that overlap on one GPU (concurrent
+ * streams, or graphs replayed concurrently) race. Arguments and results are
+ * otherwise those of gdnr_replay_fp8_split.
+ */
+int gdnr_replay_fp8_split_noalloc(const gdnr_tensor* checkpoint, const gdnr_tensor* checkpoint_scale,
+                                  const gdnr_tensor* q, const gdnr_tensor* k_cache,
+                                  const gdnr_tensor* v_cache, const gdnr_tensor* g_cache,
+                                  const gdnr_tensor* beta_cache, const gdnr_tensor* valid_len,
+                                  const gdnr_tensor* out, int32_t block_v, int32_t block_kc,
+                                  int32_t precompute_grouped, void* stream);
+
+/*
  * Full-contract preparation of one token per sequence:
  *   q,k <- x / sqrt(sum(x^2) + 1e-6) (per key head), q -> q_out[b],
  *   k -> k_ring[b, pos[b]], v (copied) -> v_ring[b, pos[b]],
