@@ -120,15 +120,6 @@ __device__ __forceinline__ uint32_t ld_u16_uniform(const uint8_t* p) {
   return (ld_u32_uniform((const void*)(ad & ~(uintptr_t)3)) >> (8u * (uint32_t)(ad & 2))) & 0xFFFFu;
 }
 __device__ __forceinline__ u32x4_t ld16(const uint8_t* p) { return *(const u32x4_t*)p; }
-// A wave-uniform pointer the compiler cannot see through: loads from it are
-// neither merged with nor hoisted above earlier loads of the same rows.
-__device__ __forceinline__ uint8_t* opaque_uniform(uint8_t* p) {
-  const uint64_t v = (uint64_t)p;
-  uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
-  uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(v >> 32));
-  asm volatile("" : "+s"(lo), "+s"(hi));
-  return (uint8_t*)(((uint64_t)hi << 32) | lo);
-}
 typedef __attribute__((address_space(1))) const u32x4_t g_u32x4;
 typedef __attribute__((address_space(1))) u32x4_t g_u32x4_w;
 // The kernel's arguments as laid out in the kernarg segment (parameters in
@@ -152,6 +143,24 @@ __device__ __forceinline__ const StepArgs& opaque_args() {
   return *(const StepArgs*)(c_args*)(((uint64_t)hi << 32) | lo);
 }
 __device__ __forceinline__ uint32_t ld32(const uint8_t* p) { return *(const uint32_t*)p; }
+// Direct global -> LDS copy of 16 bytes per lane (global_load_lds_dwordx4):
+// lane l's 16 bytes land at LDS address lds_addr + 16 l (lds_addr wave-uniform,
+// through M0, which is restored). Written as inline assembly so that the
+// compiler does not order every later LDS read after it: the caller waits for
+// it (vmcnt) before reading the destination, and the compiler's own vmcnt
+// waits, which do not count it, can only wait longer than they need.
+__device__ __forceinline__ void dma16(const uint8_t* src, uint32_t lds_addr) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %2, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(lds_addr), "v"(src)
+      : "memory");
+}
 
 // DPP move within a 16-lane row; lanes whose source is outside the row get `fill`
 template <int CTRL>
@@ -203,27 +212,32 @@ __device__ __forceinline__ float rows_reduce_scatter(float p0, float p1, float p
 
 extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
 
-// LDS of a workgroup (bytes). The chain wave writes everything before the
-// workgroup barrier; the row waves only read it after.
+// LDS of a workgroup (bytes). A unit's chain wave writes its blocks before
+// it sets the unit's flag; the unit's row waves only read them after.
 constexpr int kXStride = 272;                  // X row stride (256 + 16: conflict-free operand reads)
 constexpr int kLX = 0;                         // X rows [16][kXStride], the A operand in row form
 constexpr int kLQK = kLX + 16 * kXStride;      // the prepared q and k rows [2][256] (pair layout = row form)
 constexpr int kLKT = kLQK + 512;               // K^T operand tiles [8][16][16] act (flush)
 constexpr int kLG = kLKT + 8 * 16 * 16 * 2;    // Gram rows f32 [16][16]
 constexpr int kLDq = kLG + 1024;               // k_t . q of a full ring f32 [16]
-constexpr int kLHeads = kLDq + 64;             // per value head blocks
+constexpr int kLFlag = kLDq + 64;              // int [16]: the unit's flags (kFlag* below)
+constexpr int kLHeads = kLFlag + 64;           // per value head blocks
+constexpr int kFlagReady = 0;                  // the chain wave's LDS blocks are complete
 // per value head (offsets from the head's block)
 constexpr int kHCoef = 0;                      // f32 [16]: c_t (replay)
 constexpr int kHLam = kHCoef + 64;             // f32 [4]: lam, the scale of the T_0 rows
 constexpr int kHFac = kHLam + 16;              // float4 [16]: (pre, post, dq, 0) (flush)
 constexpr int kHT0 = kHFac + 256;              // act [3][128]: T_0 as hi, mid and lo rows (replay)
-constexpr int kHR = kHT0 + 768;                // f32 [16][16]: R = (I + M)^-1 (flush)
-constexpr int kHM = kHR + 1024;                // f32 [16][16]: M (chain scratch)
-constexpr int kHeadLds = kHM + 1024;
+constexpr int kHM = kHT0;                      // f32 [16][16]: M (chain scratch; flush, so T_0's bytes)
+constexpr int kHR = kHM + 1024;                // f32 [16][16]: R = (I + M)^-1 (flush)
+constexpr int kHeadLds = kHR + 1024;
 constexpr int kMaxDecodeHeads = 2;            // value heads per unit (gw)
 constexpr int kUnitBase = kLHeads + kMaxDecodeHeads * kHeadLds;  // LDS of one unit before its v rows
-// then the v rows of each of its row waves, token-major: [16][32 vb + 16] bytes
-__host__ __device__ constexpr int unit_lds(int rpu, int vb) { return kUnitBase + rpu * kStepRing * (64 * vb + 16); }
+// then per row wave: its v rows, token-major ([16][64 vb + 16] bytes), and
+// the flush's prefetch buffer of one vblock's codes (4 blocks of 64 x 16 bytes)
+constexpr int kVblockBytes = 4 * 64 * 16;
+__host__ __device__ constexpr int row_wave_lds(int vb) { return kStepRing * (64 * vb + 16) + kVblockBytes; }
+__host__ __device__ constexpr int unit_lds(int rpu, int vb) { return kUnitBase + rpu * row_wave_lds(vb); }
 
 // raw bits of a gating input (f32, or the activation dtype) and their value
 template <bool GATE_F32>
@@ -251,6 +265,9 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
     uint8_t* ckpt, uint8_t* kring, uint32_t ck_b, uint32_t ck_h, uint32_t ck_v, uint32_t k_b, uint32_t k_t,
     uint32_t k_h, int32_t L, int32_t G, int32_t shape, const StepArgs a) {
   constexpr int ES = 2;
+  constexpr int RPW = 16 * TPW;           // V-rows per row wave
+  constexpr int VB = TPW / 2;             // vblocks (32 rows) per row wave
+  constexpr int VSTRIDE = RPW * ES + 16;  // LDS bytes per token of a row wave's v rows
   const int lane = threadIdx.x & 63;
   const int q4 = lane >> 4, l16 = lane & 15;
   const int w = uni(threadIdx.x >> 6);
@@ -310,6 +327,9 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
     // (the sequence index through opaque_s: addresses from the argument block
     // are formed here, not in code shared with the row waves)
     const int b = opaque_s(b0);
+    // the unit's flags start clear; the row waves read them only after barrier 1
+    if (lane < 16) ((volatile int*)(ul + kLFlag))[lane] = 0;
+    GDNR_WAIT_LGKM0();
     // Lane (t = l16, row q4). For the gates, the coefficient chain and the
     // flush factors, row j holds value head hv0 + j of the unit (rows at or
     // past gw repeat the last head and publish nothing): the heads advance in
@@ -571,18 +591,15 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
         for (int t = 0; t < NT; ++t) Rj[t * NT + l16] = (t < n && on) ? r[t] : 0.f;
       }
     }
-    // everything is in LDS before the barrier
+    // everything is in LDS before the flag
     GDNR_WAIT_LGKM0();
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_barrier();
+    if (lane == 0)
+      __hip_atomic_store((int*)(ul + kLFlag) + kFlagReady, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
     return;
   }
 
   // ================= row waves ====================================================
   const int b = opaque_s(b0);
-  constexpr int RPW = 16 * TPW;  // V-rows per wave
-  constexpr int VB = TPW / 2;     // vblocks (32 rows) per wave
-  constexpr int VSTRIDE = RPW * ES + 16;  // LDS bytes per token of the wave's v rows
   const int wr = (w - U) - u * rpu;
   const int j = uni(wr / NWH), part = wr - j * NWH;  // value head in the unit, row block of it
   // (barrier 1: every chain wave's requests go first)
@@ -592,20 +609,29 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
   const int hv = hv0 + j;
   const int R0 = RPW * part;
   const uint8_t* hl = ul + kLHeads + j * kHeadLds;
-  // ---- checkpoint rows of the wave's tiles (preloaded arguments only)
+  // ---- checkpoint rows of the wave's tiles (preloaded arguments only):
+  // vblock 0 (both branches start with it), then the sequence's metadata;
+  // the other tiles only for the replay (the flush reads each vblock in turn,
+  // and a wave with fewer loads in the memory pipeline gets to its first
+  // vblock sooner)
   uint8_t* ck_rows = ckpt + (bs * ck_b + hv * ck_h + R0 * ck_v);
   u32x4_t cw[TPW][2];
-#pragma unroll
-  for (int i = 0; i < TPW; ++i) {
+  auto load_tile = [&](int i) {
     const uint32_t off = (uint32_t)(32 * (i >> 1) + 2 * l16 + (i & 1)) * ck_v + 32 * q4;
     cw[i][0] = *(g_u32x4*)(ck_rows + off);
     cw[i][1] = *(g_u32x4*)(ck_rows + off + 16);
-  }
+  };
+  load_tile(0);
+  load_tile(1);
   GDNR_COMPILER_FENCE();
   const StepArgs& A = opaque_args();
   int n, pos;
   bool do_flush;
   read_meta(A, n, pos, do_flush);
+  if (!do_flush) {
+#pragma unroll
+    for (int i = 2; i < TPW; ++i) load_tile(i);
+  }
   uint8_t* scale_hv = A.scale + (bs * A.sc_b + hv * A.sc_h);
   const int vb0 = R0 / kVBlock;
   float sct[VB];  // the vblock scales
@@ -633,15 +659,17 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
     }
   }
   GDNR_COMPILER_FENCE();
-  // the chain wave's LDS blocks are complete after the barrier
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
+  // the chain wave's LDS blocks are complete once its flag is set (a flag,
+  // not a workgroup barrier: the waves of a flushing unit need not wait for
+  // the other units' row waves to get their loads issued)
+  wait_flag((int*)(ul + kLFlag) + kFlagReady, A.status);
 
   // ring append of the new token's v rows (full contract; this wave's rows,
-  // which no other wave reads): the lanes that loaded token pos
+  // which no other wave reads): the lanes that loaded token pos. (The flush
+  // appends from LDS after its loop: no store is outstanding when the loop
+  // starts, so its waits for each vblock's codes never cover a store.)
   if constexpr (FUSED) {
-    if (pos >= 0) {
+    if (pos >= 0 && !do_flush) {
       uint8_t* vw = A.v + (bs * A.v_b + (uint32_t)pos * A.v_t + hv * A.v_h + R0 * ES) + 16 * vpiece;
 #pragma unroll
       for (int k = 0; k < NVL; ++k)
@@ -651,7 +679,7 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
   // the v rows go to LDS token-major ([16][VS] bytes; the replay once its
   // products are issued, the flush first): lane (nn, q4) then reads the two
   // rows of tiles (2p, 2p + 1) of token 4 q4 + e as one word
-  uint8_t* vl = ul + kUnitBase + wr * (NT * VSTRIDE);
+  uint8_t* vl = ul + kUnitBase + wr * row_wave_lds(VB);
   auto stage_v = [&]() {
 #pragma unroll
     for (int k = 0; k < NVL; ++k) *(u32x4_t*)(vl + vtok(k) * VSTRIDE + 16 * vpiece) = vq[k];
@@ -740,12 +768,31 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
     return u32x4_t{h2 & (d0 | d1), h2 & (d2 | d3), l2 & (d0 | d1), l2 & (d2 | d3)};
   };
   u32x4_t cur[2][2] = {{cw[0][0], cw[0][1]}, {cw[1][0], cw[1][1]}};
-  const uint8_t* rows_again = opaque_uniform(ck_rows);
+  // The codes of vblock p + 1 come from the wave's prefetch buffer, which
+  // direct DMA fills while vblock p - 1 is finished and p is rebuilt: block
+  // k = 2 ii + hh, lane (nn, q4) holds bytes [32 q4 + 16 hh, +16) of row
+  // 32 p + 2 nn + ii, the layout of cur[ii][hh]. Each iteration issues its
+  // DMA and then exactly 4 stores, so "4 outstanding" means the DMA of the
+  // iteration before has landed (the first iteration's, issued before the
+  // loop, is the only request outstanding).
+  uint8_t* const pf = vl + NT * VSTRIDE;
+  const uint32_t pf_addr = (uint32_t)uni((int)(uint32_t)(uintptr_t)pf);
+  auto prefetch = [&](int pv) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      dma16(ck_rows + (uint32_t)(32 * pv + 2 * l16 + (k >> 1)) * ck_v + 32 * q4 + 16 * (k & 1), pf_addr + 1024 * k);
+  };
+  // (tiles 0 and 1 have landed: stage_v waited for the v rows, read after them)
+  if (VB > 1) prefetch(1);
   // (a loop, not unrolled: one vblock's registers at a time; the indices
   // that depend on p are formed by selects, not by indexing registers)
   float opart_all[TPW];
 #pragma unroll
   for (int i = 0; i < TPW; ++i) opart_all[i] = 0.f;
+  // the new vblock scales, lane p holding vblock p's: stored after the loop,
+  // so that the loop's only memory requests are the codes it reads and
+  // writes (its waits for the next vblock's codes then never cover a store)
+  uint32_t new_scale = 0;
 #pragma unroll 1
   for (int p = 0; p < VB; ++p) {
     float scp = sct[0];
@@ -843,24 +890,24 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
         }
       }
     }
-    // the next vblock's codes, read (into the same registers) while this
-    // one is requantised
+    // the next vblock's codes from the prefetch buffer (into the same
+    // registers), then the buffer refilled with the one after
     if (p + 1 < VB) {
+      if (p == 0) GDNR_WAIT_VMCNT(0);
+      else GDNR_WAIT_VMCNT(4);
 #pragma unroll
-      for (int ii = 0; ii < 2; ++ii) {
-        const uint32_t off = (uint32_t)(32 * (p + 1) + 2 * l16 + ii) * ck_v + 32 * q4;
-        cur[ii][0] = *(g_u32x4*)(rows_again + off);
-        cur[ii][1] = *(g_u32x4*)(rows_again + off + 16);
-      }
+      for (int k = 0; k < 4; ++k) cur[k >> 1][k & 1] = *(const u32x4_t*)(pf + 1024 * k + 16 * lane);
+      GDNR_WAIT_LGKM0();
+      if (p + 2 < VB) prefetch(p + 2);
     }
     const uint32_t amb = wave_max_u32(__float_as_uint(am));
     // the reference quantiser (ref:36-37,83-99): s = amax / 448 (1 when amax
     // is not > 0); codes = e4m3fn(clamp(x / s, +-448)) with the unrounded s;
-    // the quotient by quotient_rn when the block is finite
+    // the quotient by quotient_f64 when the block is finite
     const float amax = __uint_as_float(amb);
     const float s32 = (amax > 0.0f) ? amax / 448.0f : 1.0f;
     const bool fast = quotient_fast(amb, s32);
-    const float rcp = 1.0f / s32;
+    const double r64 = 1.0 / (double)s32;
     // pass 2: the kept column groups requantised and stored (the division
     // path of non-finite or tiny-scale blocks is a loop of its own)
     auto pass2 = [&](auto quant) {
@@ -878,8 +925,8 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
     };
     if (uni((int)fast) != 0) {
       pass2([&](const f32x4_t& v) {
-        return f32x4_to_fp8(quotient_rn(v[0], s32, rcp), quotient_rn(v[1], s32, rcp), quotient_rn(v[2], s32, rcp),
-                            quotient_rn(v[3], s32, rcp));
+        return f32x4_to_fp8(quotient_f64(v[0], r64), quotient_f64(v[1], r64), quotient_f64(v[2], r64),
+                            quotient_f64(v[3], r64));
       });
     } else {
       // (one quotient at a time: this path is rare and should hold few registers)
@@ -896,11 +943,18 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
         return wd;
       });
     }
-    if (lane == 0) *(uint16_t*)(scale_hv + (vb0 + p) * A.sc_v) = __builtin_bit_cast(uint16_t, (_Float16)s32);
+    new_scale = lane == p ? (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)s32) : new_scale;
   }
 #pragma unroll
   for (int g = 0; g < TPW / 4; ++g)
     store_out(g, opart_all[4 * g], opart_all[4 * g + 1], opart_all[4 * g + 2], opart_all[4 * g + 3]);
+  if (lane < VB) *(uint16_t*)(scale_hv + (vb0 + lane) * A.sc_v) = (uint16_t)new_scale;
+  if constexpr (FUSED) {
+    if (pos >= 0 && lane < CPT) {
+      uint8_t* vw = A.v + (bs * A.v_b + (uint32_t)pos * A.v_t + hv * A.v_h + R0 * ES) + 16 * lane;
+      *(u32x4_t*)vw = *(const u32x4_t*)(vl + pos * VSTRIDE + 16 * lane);
+    }
+  }
 }
 
 template <int TPW, int NWH, bool FUSED, bool GATE_F32, bool SLOTS>

@@ -200,6 +200,15 @@ __device__ __forceinline__ float quotient_rn(float x, float s, float r) {
   q = fmaf(-fmaf(q, s, -x), r, q);
   return q;
 }
+// The same correctly rounded x / s from one double product, r64 = RN64(1 / s):
+// q = RN32(RN64(x r64)). The double product is within 2^-52 (relative) of
+// x / s. Where x / s is a normal float it is a quotient of two 24-bit
+// significands, which is never an f32 rounding midpoint and lies at least
+// 2^-50 (relative) from every one (|x - s m| >= 2^(a - 26) for x = X 2^a and
+// any midpoint m within a factor 2 of x / s), so the product rounds to the
+// same float. Smaller quotients (|x / s| < 2^-126) round to +-0 in e4m3 either
+// way, with the sign of x. Used under the same conditions as quotient_rn.
+__device__ __forceinline__ float quotient_f64(float x, double r64) { return (float)((double)x * r64); }
 // Whether a block with this amax (bits of |x| max) and scale takes quotient_rn:
 // amax finite and s >= 2^-64.
 __device__ __forceinline__ bool quotient_fast(uint32_t amax_bits, float s) {
@@ -257,6 +266,35 @@ __device__ __forceinline__ int wave_sum_i32(int x) {
   x += (int)dpp_u<kDppBcast15, 0xA>((uint32_t)x);
   x += (int)dpp_u<kDppBcast31, 0xC>((uint32_t)x);
   return __builtin_amdgcn_readlane(x, 63);
+}
+
+// ---------------------------------------------------------------- LDS flags
+// Acquire-load of an LDS flag, made wave-uniform: every lane reads the same
+// word, and a uniform loop exit keeps the polling loops out of the CFG
+// structurizer (which would otherwise merge the code after them).
+__device__ __forceinline__ bool flag_set(int* f) {
+  return __builtin_amdgcn_readfirstlane(__hip_atomic_load(f, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP)) != 0;
+}
+// bounded wait for an LDS flag; a wait that gives up is counted in the
+// device status word (gdnr_wait_timeouts) and reported to the caller
+__device__ __forceinline__ bool wait_flag(int* f, uint32_t* status) {
+  for (int it = 0; it < (1 << 22); ++it) {
+    if (flag_set(f)) return true;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  if ((threadIdx.x & 63) == 0 && status) atomicAdd(status, 1u);
+  return false;
+}
+
+// bounded wait for an LDS counter to reach `target` (counted like wait_flag)
+__device__ __forceinline__ bool wait_count(int* f, int target, uint32_t* status) {
+  for (int it = 0; it < (1 << 22); ++it) {
+    if (__builtin_amdgcn_readfirstlane(__hip_atomic_load(f, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP)) >= target)
+      return true;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  if ((threadIdx.x & 63) == 0 && status) atomicAdd(status, 1u);
+  return false;
 }
 
 // ---------------------------------------------------------------- waits

@@ -130,23 +130,6 @@ __device__ __forceinline__ int xr_off_row(int lds_k, int lds_knew, int lds_q, in
   return x < n ? (x == pos ? lds_knew + by : lds_k + kr_off<ROWB>(x, by)) : lds_q + by;
 }
 
-// Acquire-load of an LDS flag, made wave-uniform: every lane reads the same
-// word, and a uniform loop exit keeps the polling loops out of the CFG
-// structurizer (which would otherwise merge the replay and flush tails).
-__device__ __forceinline__ bool flag_set(int* f) {
-  return __builtin_amdgcn_readfirstlane(__hip_atomic_load(f, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP)) != 0;
-}
-// bounded wait for an LDS flag; a wait that gives up is counted in the
-// device status word (gdnr_wait_timeouts) and reported to the caller
-__device__ __forceinline__ bool wait_flag(int* f, uint32_t* status) {
-  for (int it = 0; it < (1 << 22); ++it) {
-    if (flag_set(f)) return true;
-    __builtin_amdgcn_s_sleep(1);
-  }
-  if ((threadIdx.x & 63) == 0 && status) atomicAdd(status, 1u);
-  return false;
-}
-
 // raw bits of a gating input (f32, or the activation dtype) and their value
 template <bool GATE_F32, class Act>
 __device__ __forceinline__ uint32_t ld_gate_bits(const uint8_t* p) {
