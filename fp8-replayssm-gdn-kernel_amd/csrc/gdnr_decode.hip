@@ -223,20 +223,41 @@ constexpr int kLDq = kLG + 1024;               // k_t . q of a full ring f32 [16
 constexpr int kLFlag = kLDq + 64;              // int [16]: the unit's flags (kFlag* below)
 constexpr int kLHeads = kLFlag + 64;           // per value head blocks
 constexpr int kFlagReady = 0;                  // the chain wave's LDS blocks are complete
+constexpr int kFlagVStaged = 4;                // + w: row wave w's v rows are in LDS (flush)
+constexpr int kFlagHelped = 8;                 // + w: vblocks of row wave w rebuilt by helpers (flush)
 // per value head (offsets from the head's block)
 constexpr int kHCoef = 0;                      // f32 [16]: c_t (replay)
 constexpr int kHLam = kHCoef + 64;             // f32 [4]: lam, the scale of the T_0 rows
 constexpr int kHFac = kHLam + 16;              // float4 [16]: (pre, post, dq, 0) (flush)
 constexpr int kHT0 = kHFac + 256;              // act [3][128]: T_0 as hi, mid and lo rows (replay)
-constexpr int kHM = kHT0;                      // f32 [16][16]: M (chain scratch; flush, so T_0's bytes)
+constexpr int kHM = kHT0;                      // f32 [16][16]: M (chain scratch; flush, so T_0's bytes;
+                                               // then the helpers' o partials, [2][64] float2)
 constexpr int kHR = kHM + 1024;                // f32 [16][16]: R = (I + M)^-1 (flush)
 constexpr int kHeadLds = kHR + 1024;
 constexpr int kMaxDecodeHeads = 2;            // value heads per unit (gw)
 constexpr int kUnitBase = kLHeads + kMaxDecodeHeads * kHeadLds;  // LDS of one unit before its v rows
 // then per row wave: its v rows, token-major ([16][64 vb + 16] bytes), and
-// the flush's prefetch buffer of one vblock's codes (4 blocks of 64 x 16 bytes)
+// two buffers of one vblock's codes for the flush (4 blocks of 64 x 16
+// bytes): the row wave's prefetch, and a helper's
 constexpr int kVblockBytes = 4 * 64 * 16;
-__host__ __device__ constexpr int row_wave_lds(int vb) { return kStepRing * (64 * vb + 16) + kVblockBytes; }
+__host__ __device__ constexpr int row_wave_lds(int vb) { return kStepRing * (64 * vb + 16) + 2 * kVblockBytes; }
+// Vblocks of each row wave of a flushing unit that helpers rebuild (the
+// last ones), given nhelp helper waves: the smallest longest chain
+// max(vb - k, ceil(rpu k / nhelp)), at most one per helper (each helper job
+// needs a buffer: the helped row wave's, or the partner unit's second).
+// nhelp is 0 when the partner unit flushes too: the workgroup's SIMDs are
+// then busy with row waves, and a helper only lengthens the launch.
+__device__ __forceinline__ int helper_vblocks(int vb, int rpu, int nhelp) {
+  int best = vb, kb = 0;
+  for (int k = 1; k < vb && k <= nhelp; ++k) {
+    const int crit = max(vb - k, (rpu * k + nhelp - 1) / nhelp);
+    if (crit < best) {
+      best = crit;
+      kb = k;
+    }
+  }
+  return kb;
+}
 __host__ __device__ constexpr int unit_lds(int rpu, int vb) { return kUnitBase + rpu * row_wave_lds(vb); }
 
 // raw bits of a gating input (f32, or the activation dtype) and their value
@@ -322,6 +343,199 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
     decode_meta(load_meta(A, opaque_s(b0)), n, pos, do_flush);
   };
 
+  // ---- the flush's rebuild of one vblock: 32 V-rows (tiles ii = 0, 1: rows
+  // 32 p + 2 nn + ii of a row wave's block) on every ring token: P = X S_0^T,
+  // W = v - pre P, U = R W, U~ = post U, then S_n = lam S_0 + K^T U~ by 16 x 4
+  // column groups kept in registers; the vblock amax and o = S_n q as the
+  // groups complete, then the requantisation in place. A row wave rebuilds
+  // its own vblocks with it, and a chain wave whose chain is published
+  // rebuilds the last ones of a flushing unit's row waves (the helpers
+  // below). uu: the unit's LDS block, hb: the head's, vr: the row wave's v
+  // rows, nf: the ring fill, c: the vblock's codes (cur layout), scp: its
+  // scale, rows: the row wave's checkpoint rows. Returns the new scale and
+  // this lane's shares op[ii] of o for the two tiles; after_pass1() runs once
+  // the codes are no longer needed.
+  //
+  // S_n column group ct of tile ii: lane (nn, q4) gets
+  // S_n[row r(ii, nn)][32 q4 + 4 ct + e], code byte 4 ct + e of its 32. lam
+  // S_0 enters through the MFMA as (ls I) S_0^T with ls = lam * scale split
+  // into hi + lo halves; each hi/lo pair is one 16x16x32 MFMA (k-slots
+  // 8 q4 + j: j < 4 the hi part, j >= 4 the lo part of column 4 q4 + (j & 3)).
+  auto flush_vblock = [&](const uint8_t* uu, const uint8_t* hb, const uint8_t* vr, int nf, const u32x4_t (&c)[2][2],
+                          float scp, uint8_t* rows, int p, float* op, auto&& after_pass1) -> float {
+    const float lamv = ((const float*)(hb + kHLam))[0];
+    u32x4_t packed[2];
+#pragma unroll
+    for (int ii = 0; ii < 2; ++ii) {
+      // P on the ring tokens, and on the query as a block of its own (row 0)
+      f32x4_t pr = {0.f, 0.f, 0.f, 0.f}, pq = pr;
+      int xo = kLX + l16 * kXStride + 64 * q4, qo = kLQK + 64 * q4;
+      asm volatile("" : "+v"(xo), "+v"(qo));  // read in the loop, not held across it
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const u32x4_t x = *(const u32x4_t*)(uu + xo + 16 * m);
+        const u32x4_t qx = *(const u32x4_t*)(uu + qo + 16 * m);
+        const u32x4_t bv = codes8(c[ii], m);
+        pr = mfma16(x, bv, pr);
+        pq = mfma16(l16 == 0 ? qx : u32x4_t{0u, 0u, 0u, 0u}, bv, pq);
+      }
+      float wv[4], post[4], dqt[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int t = 4 * q4 + e;
+        const float4 fc = *(const float4*)(hb + kHFac + 16 * t);
+        post[e] = fc.y;
+        dqt[e] = fc.z;
+        // v of token t for tile ii (zero at or past the fill)
+        const uint32_t vw = *(const uint32_t*)(vr + t * VSTRIDE + (32 * p + 2 * l16) * ES);
+        const float vv = act_val(ii ? (vw >> 16) : vw);
+        wv[e] = t < nf ? vv - fc.x * (pr[e] * scp) : 0.f;
+      }
+      const float4 rr = *(const float4*)(hb + kHR + 4 * (l16 * NT + 4 * q4));
+      const float rrv[4] = {rr.x, rr.y, rr.z, rr.w};
+      f32x4_t uv = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) uv = __builtin_amdgcn_mfma_f32_16x16x4f32(rrv[e], wv[e], uv, 0, 0, 0);
+      // o = S_n q = lam (S_0 q) + sum_t U~_t (k_t . q): this lane's share
+      float ut[4];
+      float o = (lamv * scp) * pq[0];  // (zero at lanes q4 != 0)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        ut[e] = uv[e] * post[e];
+        o = fmaf(ut[e], dqt[e], o);
+      }
+      op[ii] = o;
+      if constexpr (kBF16) {
+        // hi/lo split: U~ = hi + lo to ~16 bits, both halves bf16 operands
+        const uint32_t h01 = pack_bf16x2(ut[0], ut[1]), h23 = pack_bf16x2(ut[2], ut[3]);
+        const uint32_t l01 =
+            pack_bf16x2(ut[0] - __uint_as_float(h01 << 16), ut[1] - __uint_as_float(h01 & 0xFFFF0000u));
+        const uint32_t l23 =
+            pack_bf16x2(ut[2] - __uint_as_float(h23 << 16), ut[3] - __uint_as_float(h23 & 0xFFFF0000u));
+        packed[ii] = u32x4_t{h01, h23, l01, l23};
+      } else {
+        _Float16 hh[4], ll[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          hh[e] = (_Float16)ut[e];
+          ll[e] = (_Float16)(ut[e] - (float)hh[e]);
+        }
+        auto pk = [](_Float16 x, _Float16 y) {
+          return (uint32_t)__builtin_bit_cast(uint16_t, x) | ((uint32_t)__builtin_bit_cast(uint16_t, y) << 16);
+        };
+        packed[ii] = u32x4_t{pk(hh[0], hh[1]), pk(hh[2], hh[3]), pk(ll[0], ll[1]), pk(ll[2], ll[3])};
+      }
+    }
+    // pass 1: S_n of the vblock's 2 x 8 column groups (kept) and the vblock
+    // amax (|x| max, NaN propagating like torch.amax)
+    f32x4_t sv[2][8];
+    float am = 0.f;
+    {
+      const float ls = lamv * scp;
+      uint32_t hbits, lbits;
+      if constexpr (kBF16) {
+        hbits = f32_to_bf16(ls);
+        lbits = f32_to_bf16(ls - __uint_as_float(hbits << 16));
+      } else {
+        const _Float16 hh = (_Float16)ls;
+        hbits = __builtin_bit_cast(uint16_t, hh);
+        lbits = __builtin_bit_cast(uint16_t, (_Float16)(ls - (float)hh));
+      }
+      const uint32_t d0 = l16 == 4 * q4 ? 0xFFFFu : 0u, d1 = l16 == 4 * q4 + 1 ? 0xFFFF0000u : 0u;
+      const uint32_t d2 = l16 == 4 * q4 + 2 ? 0xFFFFu : 0u, d3 = l16 == 4 * q4 + 3 ? 0xFFFF0000u : 0u;
+      const uint32_t h2 = hbits | (hbits << 16), l2 = lbits | (lbits << 16);
+      const u32x4_t a_ls = {h2 & (d0 | d1), h2 & (d2 | d3), l2 & (d0 | d1), l2 & (d2 | d3)};
+#pragma unroll
+      for (int ct = 0; ct < 8; ++ct) {
+#pragma unroll
+        for (int ii = 0; ii < 2; ++ii) {
+          const uint2 c2 = codes4(c[ii][ct >> 2][ct & 3]);
+          const f32x4_t z = {0.f, 0.f, 0.f, 0.f};
+          const f32x4_t s0 = mfma16(a_ls, u32x4_t{c2.x, c2.y, c2.x, c2.y}, z);
+          const uint2 k2 = *(const uint2*)(uu + kLKT + 2 * ((ct * 16 + l16) * 16 + 4 * q4));
+          sv[ii][ct] = mfma16(u32x4_t{k2.x, k2.y, k2.x, k2.y}, packed[ii], s0);
+        }
+        // (a group's first product completes into its second before the
+        // next group starts: no more than one intermediate is held)
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int ct = 0; ct < 8; ++ct) {
+#pragma unroll
+        for (int ii = 0; ii < 2; ++ii) {
+          const f32x4_t sg = sv[ii][ct];
+          am = __builtin_elementwise_maximum(am, __builtin_elementwise_maximum(__builtin_fabsf(sg[0]), __builtin_fabsf(sg[1])));
+          am = __builtin_elementwise_maximum(am, __builtin_elementwise_maximum(__builtin_fabsf(sg[2]), __builtin_fabsf(sg[3])));
+        }
+      }
+    }
+    after_pass1();
+    const uint32_t amb = wave_max_u32(__float_as_uint(am));
+    // the reference quantiser (ref:36-37,83-99): s = amax / 448 (1 when amax
+    // is not > 0); codes = e4m3fn(clamp(x / s, +-448)) with the unrounded s;
+    // the quotient by quotient_f64 when the block is finite
+    const float amax = __uint_as_float(amb);
+    const float s32 = (amax > 0.0f) ? amax / 448.0f : 1.0f;
+    const bool fast = quotient_fast(amb, s32);
+    const double r64 = 1.0 / (double)s32;
+    // pass 2: the kept column groups requantised and stored (the division
+    // path of non-finite or tiny-scale blocks is a loop of its own)
+    auto pass2 = [&](auto quant) {
+#pragma unroll
+      for (int ii = 0; ii < 2; ++ii) {
+        const uint32_t ro = (uint32_t)(32 * p + 2 * l16 + ii) * ck_v + 32 * q4;
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          uint32_t wd[4];
+#pragma unroll
+          for (int w4 = 0; w4 < 4; ++w4) wd[w4] = quant(sv[ii][4 * hh + w4]);
+          *(g_u32x4_w*)(rows + ro + 16 * hh) = u32x4_t{wd[0], wd[1], wd[2], wd[3]};
+        }
+      }
+    };
+    if (uni((int)fast) != 0) {
+      pass2([&](const f32x4_t& v) {
+        return f32x4_to_fp8(quotient_f64(v[0], r64), quotient_f64(v[1], r64), quotient_f64(v[2], r64),
+                            quotient_f64(v[3], r64));
+      });
+    } else {
+      // (one quotient at a time: this path is rare and should hold few registers)
+      pass2([&](const f32x4_t& v) {
+        __builtin_amdgcn_sched_barrier(0);
+        float qv[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          qv[e] = v[e] / s32;
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        const uint32_t wd = f32x4_to_fp8_ref(qv[0], qv[1], qv[2], qv[3]);
+        __builtin_amdgcn_sched_barrier(0);
+        return wd;
+      });
+    }
+    return s32;
+  };
+  // DMA of one vblock's codes (rows 32 pv + 2 nn + ii of `rows`) into a
+  // buffer in the cur layout: block k = 2 ii + hh, lane (nn, q4) gets bytes
+  // [32 q4 + 16 hh, +16) of its row
+  auto dma_vblock = [&](const uint8_t* rows, int pv, const uint8_t* buf) {
+    const uint32_t ba = (uint32_t)uni((int)(uint32_t)(uintptr_t)buf);
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      dma16(rows + (uint32_t)(32 * pv + 2 * l16 + (k >> 1)) * ck_v + 32 * q4 + 16 * (k & 1), ba + 1024 * k);
+  };
+  // the partner unit: the same (key head, value-head group) in the
+  // workgroup's other sequence (b0 ^ 1); while it does not flush, its chain
+  // wave and buffers help a flushing unit
+  const bool has_partner = U >= 2;
+  const int up = U == 4 ? (u ^ 2) : (u ^ 1);
+  auto partner_flushes = [&](const StepArgs& A) {
+    int pn, ppos;
+    bool pfl;
+    decode_meta(load_meta(A, opaque_s(b0 ^ 1)), pn, ppos, pfl);
+    return pfl;
+  };
+
   if (chain) {
     // ================= chain wave =================================================
     // (the sequence index through opaque_s: addresses from the argument block
@@ -347,6 +561,8 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
     for (int m = 0; m < 4; ++m) xr[m] = ld16(krow + 16 * m);
     GDNR_COMPILER_FENCE();
     const MetaRaw meta = load_meta(a, b);
+    MetaRaw pmeta{};
+    if (has_partner) pmeta = load_meta(a, b ^ 1);
     uint32_t qbits, kbits = 0;
     if constexpr (FUSED) {
       const uint8_t* row = a.mixed + b * a.mx_b;
@@ -377,6 +593,51 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
     // every load above is needed next; waiting for them here keeps later
     // waits from covering the ring-append stores
     GDNR_WAIT_VMCNT(0);
+
+    // ---- flush helper, set-up: this wave rebuilds vblocks of a flushing unit
+    // v, its own (helper 0) or, while its own unit replays, the partner unit
+    // (helper 1): the last nh vblocks of each of v's row waves, jobs
+    // g = kk rpu + w (vblock VB - nh + kk of row wave w) split evenly between
+    // v's helpers. Job (kk, w) reads its codes into row wave w's second
+    // buffer, of v for kk = 0 and of v's partner for kk = 1 (a replaying
+    // unit's are unused). The DMAs and the rebuilds follow the chain's
+    // publication (issued earlier, the DMAs would sit in the memory pipeline
+    // ahead of what the chain and the row waves wait for).
+    int hv_unit = -1, h_nh = 0, h_g0 = 0, h_g1 = 0, h_nf = n, h_bs = bs;
+    {
+      int pn = 0, ppos;
+      bool pfl = false;
+      if (has_partner) decode_meta(pmeta, pn, ppos, pfl);
+      int hidx = 0, nhelp = 1;
+      if (do_flush) {
+        hv_unit = u;
+        nhelp = has_partner ? (pfl ? 0 : 2) : 1;
+      } else if (has_partner && pfl) {
+        hv_unit = up;
+        hidx = 1;
+        nhelp = 2;
+        h_nf = pn;
+        h_bs = b ^ 1;
+        if constexpr (SLOTS) {
+          const int sl = (int)uni((int)ld_u32_uniform(a.slot + (b ^ 1) * a.sl_s));
+          h_bs = (sl >= 0 && sl < a.n_slots) ? sl : 0;
+        }
+      }
+      hv_unit = uni(hv_unit);
+      if (hv_unit >= 0 && nhelp > 0) {
+        h_nh = uni(helper_vblocks(VB, rpu, nhelp));
+        const int jobs = h_nh * rpu, per = (jobs + nhelp - 1) / nhelp;
+        h_g0 = uni(hidx * per);
+        h_g1 = uni(min(jobs, h_g0 + per));
+      }
+    }
+    auto job_rows = [&](int wv) {
+      return ckpt + (h_bs * ck_b + (hv0 + wv / NWH) * ck_h + RPW * (wv % NWH) * ck_v);
+    };
+    auto job_buf = [&](int kk, int wv) {
+      const int bu = kk == 0 ? hv_unit : (hv_unit == u ? up : u);
+      return lds + bu * unit_lds(rpu, VB) + kUnitBase + wv * row_wave_lds(VB) + NT * VSTRIDE + kVblockBytes;
+    };
 
     // ---- the query (and new key) rows: normalised as the preparation does
     // (x / sqrt(sum x^2 + 1e-6), lane pairs, rounded to the ring dtype); the
@@ -595,6 +856,51 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
     GDNR_WAIT_LGKM0();
     if (lane == 0)
       __hip_atomic_store((int*)(ul + kLFlag) + kFlagReady, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+
+    // ---- flush helper, the rebuilds (each issues exactly 4 stores: with two
+    // jobs "4 outstanding" means the job's DMA has landed, with one "none")
+    if (h_g0 >= h_g1) return;
+    {
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) {
+      const int g = h_g0 + jj;
+      if (g < h_g1) dma_vblock(job_rows(g % rpu), VB - h_nh + g / rpu, job_buf(g / rpu, g % rpu));
+    }
+
+      uint8_t* const uv = lds + hv_unit * unit_lds(rpu, VB);
+      int* const vflags = (int*)(uv + kLFlag);
+      if (hv_unit != u) wait_flag(vflags + kFlagReady, a.status);
+      uint32_t nsc = 0;
+      uint8_t* sc_addr = nullptr;
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) {
+        const int g = h_g0 + jj;
+        if (g >= h_g1) break;
+        const int kk = g / rpu, wv = g % rpu, pv = VB - h_nh + kk;
+        if (h_g1 - h_g0 == 2) GDNR_WAIT_VMCNT(4);
+        else GDNR_WAIT_VMCNT(0);
+        wait_flag(vflags + kFlagVStaged + wv, a.status);
+        const uint8_t* buf = job_buf(kk, wv);
+        u32x4_t c[2][2];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) c[k >> 1][k & 1] = *(const u32x4_t*)(buf + 1024 * k + 16 * lane);
+        const int hvj = hv0 + wv / NWH, partj = wv % NWH;
+        uint8_t* const sc_j =
+            a.scale + (h_bs * a.sc_b + hvj * a.sc_h + (RPW * partj / kVBlock + pv) * a.sc_v);
+        const float scp = f16_bits_to_f32(ld_u16_uniform(sc_j));
+        const uint8_t* hbv = uv + kLHeads + (wv / NWH) * kHeadLds;
+        float op[2];
+        const float s32 =
+            flush_vblock(uv, hbv, uv + kUnitBase + wv * row_wave_lds(VB), h_nf, c, scp, job_rows(wv), pv, op, []() {});
+        *(float2*)(hbv + kHM + 512 * (partj * h_nh + kk) + 8 * lane) = make_float2(op[0], op[1]);
+        GDNR_WAIT_LGKM0();
+        if (lane == 0)
+          __hip_atomic_fetch_add(vflags + kFlagHelped + wv, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+        nsc = lane == jj ? (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)s32) : nsc;
+        sc_addr = lane == jj ? sc_j : sc_addr;
+      }
+      if (lane < h_g1 - h_g0) *(uint16_t*)sc_addr = (uint16_t)nsc;
+    }
     return;
   }
 
@@ -628,9 +934,16 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
   int n, pos;
   bool do_flush;
   read_meta(A, n, pos, do_flush);
+  // (the flush: how many of its vblocks helpers take)
+  uint8_t* const vl = ul + kUnitBase + wr * row_wave_lds(VB);
+  uint8_t* const pf = vl + NT * VSTRIDE;
+  int nh = 0;
   if (!do_flush) {
 #pragma unroll
     for (int i = 2; i < TPW; ++i) load_tile(i);
+  } else {
+    const int nhelp = has_partner ? (partner_flushes(A) ? 0 : 2) : 1;
+    nh = uni(helper_vblocks(VB, rpu, nhelp));
   }
   uint8_t* scale_hv = A.scale + (bs * A.sc_b + hv * A.sc_h);
   const int vb0 = R0 / kVBlock;
@@ -679,7 +992,6 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
   // the v rows go to LDS token-major ([16][VS] bytes; the replay once its
   // products are issued, the flush first): lane (nn, q4) then reads the two
   // rows of tiles (2p, 2p + 1) of token 4 q4 + e as one word
-  uint8_t* vl = ul + kUnitBase + wr * row_wave_lds(VB);
   auto stage_v = [&]() {
 #pragma unroll
     for (int k = 0; k < NVL; ++k) *(u32x4_t*)(vl + vtok(k) * VSTRIDE + 16 * vpiece) = vq[k];
@@ -738,52 +1050,21 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
     return;
   }
 
-  // ---- flush, one vblock (tiles 2p, 2p + 1) at a time: P = X S_0^T of its
-  // rows on every ring token, W = v - pre P, U = R W, U~ = post U, then
-  // S_n = lam S_0 + K^T U~ by 16 x 4 column groups, kept in registers: the
-  // vblock amax and o = S_n q as the groups complete, then the
-  // requantisation in place. The codes of vblock p + 1 are read again
-  // (prefetched while p is rebuilt) rather than held since the stream.
+  // ---- flush: the wave's vblocks in turn (flush_vblock); the last nh of
+  // them rebuilt by helper waves, whose o shares come back through LDS
   stage_v();
-  const float lam = ((const float*)(hl + kHLam))[0];
-  // S_n column group ct of tile i: lane (nn, q4) gets
-  // S_n[row r(i, nn)][32 q4 + 4 ct + e], code byte 4 ct + e of its 32. lam
-  // S_0 enters through the MFMA as (ls I) S_0^T with ls = lam * scale split
-  // into hi + lo halves; each hi/lo pair is one 16x16x32 MFMA (k-slots
-  // 8 q4 + j: j < 4 the hi part, j >= 4 the lo part of column 4 q4 + (j & 3)).
-  auto a_ls_of = [&](float scp) {
-    const float ls = lam * scp;
-    uint32_t hb, lb;
-    if constexpr (kBF16) {
-      hb = f32_to_bf16(ls);
-      lb = f32_to_bf16(ls - __uint_as_float(hb << 16));
-    } else {
-      const _Float16 hh = (_Float16)ls;
-      hb = __builtin_bit_cast(uint16_t, hh);
-      lb = __builtin_bit_cast(uint16_t, (_Float16)(ls - (float)hh));
-    }
-    const uint32_t d0 = l16 == 4 * q4 ? 0xFFFFu : 0u, d1 = l16 == 4 * q4 + 1 ? 0xFFFF0000u : 0u;
-    const uint32_t d2 = l16 == 4 * q4 + 2 ? 0xFFFFu : 0u, d3 = l16 == 4 * q4 + 3 ? 0xFFFF0000u : 0u;
-    const uint32_t h2 = hb | (hb << 16), l2 = lb | (lb << 16);
-    return u32x4_t{h2 & (d0 | d1), h2 & (d2 | d3), l2 & (d0 | d1), l2 & (d2 | d3)};
-  };
+  int* const flags = (int*)(ul + kLFlag);
+  if (lane == 0) __hip_atomic_store(flags + kFlagVStaged + wr, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+  const int own = VB - nh;
   u32x4_t cur[2][2] = {{cw[0][0], cw[0][1]}, {cw[1][0], cw[1][1]}};
   // The codes of vblock p + 1 come from the wave's prefetch buffer, which
-  // direct DMA fills while vblock p - 1 is finished and p is rebuilt: block
-  // k = 2 ii + hh, lane (nn, q4) holds bytes [32 q4 + 16 hh, +16) of row
-  // 32 p + 2 nn + ii, the layout of cur[ii][hh]. Each iteration issues its
-  // DMA and then exactly 4 stores, so "4 outstanding" means the DMA of the
-  // iteration before has landed (the first iteration's, issued before the
-  // loop, is the only request outstanding).
-  uint8_t* const pf = vl + NT * VSTRIDE;
-  const uint32_t pf_addr = (uint32_t)uni((int)(uint32_t)(uintptr_t)pf);
-  auto prefetch = [&](int pv) {
-#pragma unroll
-    for (int k = 0; k < 4; ++k)
-      dma16(ck_rows + (uint32_t)(32 * pv + 2 * l16 + (k >> 1)) * ck_v + 32 * q4 + 16 * (k & 1), pf_addr + 1024 * k);
-  };
+  // direct DMA fills while vblock p - 1 is finished and p is rebuilt. Each
+  // iteration issues its DMA and then exactly 4 stores, so "4 outstanding"
+  // means the DMA of the iteration before has landed (the first iteration's,
+  // issued before the loop, is the only request outstanding). (Issued here,
+  // not with vblock 0: ahead of the v rows it would delay the first vblock.)
   // (tiles 0 and 1 have landed: stage_v waited for the v rows, read after them)
-  if (VB > 1) prefetch(1);
+  if (own > 1) dma_vblock(ck_rows, 1, pf);
   // (a loop, not unrolled: one vblock's registers at a time; the indices
   // that depend on p are formed by selects, not by indexing registers)
   float opart_all[TPW];
@@ -794,161 +1075,40 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
   // writes (its waits for the next vblock's codes then never cover a store)
   uint32_t new_scale = 0;
 #pragma unroll 1
-  for (int p = 0; p < VB; ++p) {
+  for (int p = 0; p < own; ++p) {
     float scp = sct[0];
 #pragma unroll
     for (int q = 1; q < VB; ++q) scp = p == q ? sct[q] : scp;
-    u32x4_t packed[2];
+    float op[2];
+    const float s32 = flush_vblock(ul, hl, vl, n, cur, scp, ck_rows, p, op, [&]() {
+      // the next vblock's codes from the prefetch buffer (into the same
+      // registers), then the buffer refilled with the one after
+      if (p + 1 < own) {
+        if (p == 0) GDNR_WAIT_VMCNT(0);
+        else GDNR_WAIT_VMCNT(4);
 #pragma unroll
-    for (int ii = 0; ii < 2; ++ii) {
-      const int i = 2 * p + ii;
-      // P on the ring tokens, and on the query as a block of its own (row 0)
-      f32x4_t pr = {0.f, 0.f, 0.f, 0.f}, pq = pr;
-      int xo = kLX + l16 * kXStride + 64 * q4, qo = kLQK + 64 * q4;
-      asm volatile("" : "+v"(xo), "+v"(qo));  // read in the loop, not held across it
-#pragma unroll
-      for (int m = 0; m < 4; ++m) {
-        const u32x4_t x = *(const u32x4_t*)(ul + xo + 16 * m);
-        const u32x4_t qx = *(const u32x4_t*)(ul + qo + 16 * m);
-        const u32x4_t bv = codes8(cur[ii], m);
-        pr = mfma16(x, bv, pr);
-        pq = mfma16(l16 == 0 ? qx : u32x4_t{0u, 0u, 0u, 0u}, bv, pq);
+        for (int k = 0; k < 4; ++k) cur[k >> 1][k & 1] = *(const u32x4_t*)(pf + 1024 * k + 16 * lane);
+        GDNR_WAIT_LGKM0();
+        if (p + 2 < own) dma_vblock(ck_rows, p + 2, pf);
       }
-      float wv[4], post[4], dqt[4];
+    });
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int t = 4 * q4 + e;
-        const float4 fc = *(const float4*)(hl + kHFac + 16 * t);
-        post[e] = fc.y;
-        dqt[e] = fc.z;
-        const float vv = vval(i, e);
-        wv[e] = t < n ? vv - fc.x * (pr[e] * scp) : 0.f;
-      }
-      const float4 rr = *(const float4*)(hl + kHR + 4 * (l16 * NT + 4 * q4));
-      const float rrv[4] = {rr.x, rr.y, rr.z, rr.w};
-      f32x4_t u = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) u = __builtin_amdgcn_mfma_f32_16x16x4f32(rrv[e], wv[e], u, 0, 0, 0);
-      // o = S_n q = lam (S_0 q) + sum_t U~_t (k_t . q): this lane's share
-      float ut[4];
-      float op = (lam * scp) * pq[0];  // (zero at lanes q4 != 0)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        ut[e] = u[e] * post[e];
-        op = fmaf(ut[e], dqt[e], op);
-      }
-#pragma unroll
-      for (int k = 0; k < TPW; ++k) opart_all[k] = k == i ? op : opart_all[k];
-      if constexpr (kBF16) {
-        // hi/lo split: U~ = hi + lo to ~16 bits, both halves bf16 operands
-        const uint32_t h01 = pack_bf16x2(ut[0], ut[1]), h23 = pack_bf16x2(ut[2], ut[3]);
-        const uint32_t l01 =
-            pack_bf16x2(ut[0] - __uint_as_float(h01 << 16), ut[1] - __uint_as_float(h01 & 0xFFFF0000u));
-        const uint32_t l23 =
-            pack_bf16x2(ut[2] - __uint_as_float(h23 << 16), ut[3] - __uint_as_float(h23 & 0xFFFF0000u));
-        packed[ii] = u32x4_t{h01, h23, l01, l23};
-      } else {
-        _Float16 hh[4], ll[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          hh[e] = (_Float16)ut[e];
-          ll[e] = (_Float16)(ut[e] - (float)hh[e]);
-        }
-        auto pk = [](_Float16 x, _Float16 y) {
-          return (uint32_t)__builtin_bit_cast(uint16_t, x) | ((uint32_t)__builtin_bit_cast(uint16_t, y) << 16);
-        };
-        packed[ii] = u32x4_t{pk(hh[0], hh[1]), pk(hh[2], hh[3]), pk(ll[0], ll[1]), pk(ll[2], ll[3])};
-      }
-    }
-    // pass 1: S_n of the vblock's 2 x 8 column groups (kept) and the vblock
-    // amax (|x| max, NaN propagating like torch.amax)
-    f32x4_t sv[2][8];
-    float am = 0.f;
-    {
-      const u32x4_t a_ls = a_ls_of(scp);
-#pragma unroll
-      for (int ct = 0; ct < 8; ++ct) {
-#pragma unroll
-        for (int ii = 0; ii < 2; ++ii) {
-          const uint2 c2 = codes4(cur[ii][ct >> 2][ct & 3]);
-          const f32x4_t z = {0.f, 0.f, 0.f, 0.f};
-          const f32x4_t s0 = mfma16(a_ls, u32x4_t{c2.x, c2.y, c2.x, c2.y}, z);
-          const uint2 k2 = *(const uint2*)(ul + kLKT + 2 * ((ct * 16 + l16) * 16 + 4 * q4));
-          sv[ii][ct] = mfma16(u32x4_t{k2.x, k2.y, k2.x, k2.y}, packed[ii], s0);
-        }
-        // (a group's first product completes into its second before the
-        // next group starts: no more than one intermediate is held)
-        __builtin_amdgcn_sched_barrier(0);
-      }
-#pragma unroll
-      for (int ct = 0; ct < 8; ++ct) {
-#pragma unroll
-        for (int ii = 0; ii < 2; ++ii) {
-          const f32x4_t sg = sv[ii][ct];
-          am = __builtin_elementwise_maximum(am, __builtin_elementwise_maximum(__builtin_fabsf(sg[0]), __builtin_fabsf(sg[1])));
-          am = __builtin_elementwise_maximum(am, __builtin_elementwise_maximum(__builtin_fabsf(sg[2]), __builtin_fabsf(sg[3])));
-        }
-      }
-    }
-    // the next vblock's codes from the prefetch buffer (into the same
-    // registers), then the buffer refilled with the one after
-    if (p + 1 < VB) {
-      if (p == 0) GDNR_WAIT_VMCNT(0);
-      else GDNR_WAIT_VMCNT(4);
-#pragma unroll
-      for (int k = 0; k < 4; ++k) cur[k >> 1][k & 1] = *(const u32x4_t*)(pf + 1024 * k + 16 * lane);
-      GDNR_WAIT_LGKM0();
-      if (p + 2 < VB) prefetch(p + 2);
-    }
-    const uint32_t amb = wave_max_u32(__float_as_uint(am));
-    // the reference quantiser (ref:36-37,83-99): s = amax / 448 (1 when amax
-    // is not > 0); codes = e4m3fn(clamp(x / s, +-448)) with the unrounded s;
-    // the quotient by quotient_f64 when the block is finite
-    const float amax = __uint_as_float(amb);
-    const float s32 = (amax > 0.0f) ? amax / 448.0f : 1.0f;
-    const bool fast = quotient_fast(amb, s32);
-    const double r64 = 1.0 / (double)s32;
-    // pass 2: the kept column groups requantised and stored (the division
-    // path of non-finite or tiny-scale blocks is a loop of its own)
-    auto pass2 = [&](auto quant) {
-#pragma unroll
-      for (int ii = 0; ii < 2; ++ii) {
-        const uint32_t ro = (uint32_t)(32 * p + 2 * l16 + ii) * ck_v + 32 * q4;
-#pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-          uint32_t wd[4];
-#pragma unroll
-          for (int w4 = 0; w4 < 4; ++w4) wd[w4] = quant(sv[ii][4 * hh + w4]);
-          *(g_u32x4_w*)(ck_rows + ro + 16 * hh) = u32x4_t{wd[0], wd[1], wd[2], wd[3]};
-        }
-      }
-    };
-    if (uni((int)fast) != 0) {
-      pass2([&](const f32x4_t& v) {
-        return f32x4_to_fp8(quotient_f64(v[0], r64), quotient_f64(v[1], r64), quotient_f64(v[2], r64),
-                            quotient_f64(v[3], r64));
-      });
-    } else {
-      // (one quotient at a time: this path is rare and should hold few registers)
-      pass2([&](const f32x4_t& v) {
-        __builtin_amdgcn_sched_barrier(0);
-        float qv[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          qv[e] = v[e] / s32;
-          __builtin_amdgcn_sched_barrier(0);
-        }
-        const uint32_t wd = f32x4_to_fp8_ref(qv[0], qv[1], qv[2], qv[3]);
-        __builtin_amdgcn_sched_barrier(0);
-        return wd;
-      });
-    }
+    for (int k = 0; k < TPW; ++k) opart_all[k] = k == 2 * p ? op[0] : (k == 2 * p + 1 ? op[1] : opart_all[k]);
     new_scale = lane == p ? (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)s32) : new_scale;
+  }
+  if (nh > 0) {
+    wait_count(flags + kFlagHelped + wr, nh, A.status);
+    for (int kk = 0; kk < nh; ++kk) {
+      const int p = own + kk;
+      const float2 o2 = *(const float2*)(hl + kHM + 512 * (part * nh + kk) + 8 * lane);
+#pragma unroll
+      for (int k = 0; k < TPW; ++k) opart_all[k] = k == 2 * p ? o2.x : (k == 2 * p + 1 ? o2.y : opart_all[k]);
+    }
   }
 #pragma unroll
   for (int g = 0; g < TPW / 4; ++g)
     store_out(g, opart_all[4 * g], opart_all[4 * g + 1], opart_all[4 * g + 2], opart_all[4 * g + 3]);
-  if (lane < VB) *(uint16_t*)(scale_hv + (vb0 + lane) * A.sc_v) = (uint16_t)new_scale;
+  if (lane < own) *(uint16_t*)(scale_hv + (vb0 + lane) * A.sc_v) = (uint16_t)new_scale;
   if constexpr (FUSED) {
     if (pos >= 0 && lane < CPT) {
       uint8_t* vw = A.v + (bs * A.v_b + (uint32_t)pos * A.v_t + hv * A.v_h + R0 * ES) + 16 * lane;
