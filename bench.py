@@ -50,8 +50,9 @@ for _p in (REPO, PKG):
 
 METRIC = "µs per GDN-layer decode step (B=64, L=16) + achieved HBM GB/s % of peak"
 HBM_PEAK_GBS = 8000.0
-KERNEL_NAME = "step_kernel<ActBF16, 16, true, {gate_f32}, false>"  # <act, NCH, fused, gate_f32, slots>
+KERNEL_NAME = "decode_kernel<8, 1, true, {gate_f32}, false>"  # <tiles per row wave, row waves per head, fused, gate_f32, slots>
 CPU_SAMPLE_SECONDS = 10.0
+EXTRAS = ("core", "config1", "split", "config3", "floor")
 CPU_MAX_CYCLES = 8
 
 
@@ -83,6 +84,11 @@ def parse_args():
                    help="skip the timing of the same cycle through the slot-indexed cache")
     p.add_argument("--profile", action="store_true",
                    help="short run for rocprofv3: no CPU baseline, few rounds")
+    p.add_argument("--no-extras", action="store_true",
+                   help="skip the extra measurements (core-kernel cycles, config 1, split vs fused, config 3, "
+                        "stream floor)")
+    p.add_argument("--only", choices=EXTRAS, default=None,
+                   help="run one extra measurement alone (no headline), e.g. under rocprofv3")
     return p.parse_args()
 
 
@@ -98,11 +104,36 @@ def traffic_from_profiles(batch: int, window: int):
         return None
 
 
+def host_cpu() -> dict:
+    """The host's CPU as lscpu reports it: model, sockets x cores x threads."""
+    import subprocess
+
+    info = {}
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=20).stdout
+        for line in out.splitlines():
+            key, _, val = line.partition(":")
+            info[key.strip()] = val.strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+
+    def num(key):
+        try:
+            return int(info.get(key, ""))
+        except ValueError:
+            return None
+
+    return {"model": info.get("Model name"), "sockets": num("Socket(s)"), "cores_per_socket": num("Core(s) per socket"),
+            "threads_per_core": num("Thread(s) per core"), "logical_cpus": os.cpu_count()}
+
+
 def cpu_baseline(args, shape, window):
     """Time the reference's host path on a batch sample; scale to the full batch."""
     import torch
 
     from oracle import cpu_torch_path
+
+    torch.set_num_threads(os.cpu_count() or 1)      # every host thread, as the reference's CPU run would use
 
     sample = max(1, min(args.cpu_sample, args.batch))
     gen = torch.Generator().manual_seed(1)
@@ -129,10 +160,14 @@ def cpu_baseline(args, shape, window):
             break
     us_per_step = elapsed / (cycles * window) * 1e6 * (args.batch / sample)
     scaled = f"; scaled x{args.batch / sample:g} to batch {args.batch}" if sample != args.batch else ""
+    host = host_cpu()
     return {
         "value": us_per_step,
         "unit": "us/step",
         "cores": threads,
+        "threads": threads,
+        "host": host,
+        "torch": torch.__version__,
         "kind": "port",
         "sample": (f"{cycles} whole ring cycle(s) ({cycles * window} steps incl. {cycles} flushes) at batch {sample}, "
                    f"same layer shape and cycle as the GPU run, fp32 torch on {threads} host threads, "
@@ -158,6 +193,10 @@ def main() -> int:
         return 1
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)
+    if args.only:
+        stream = torch.cuda.Stream(device)       # default priority
+        print(json.dumps({"only": args.only, **run_extras([args.only], device, stream)}), flush=True)
+        return 0
     B, L, S = args.batch, args.window, args.sets
     shape = synth.Shape(B)
     traffic_shape = LayerShape(B)
@@ -299,8 +338,10 @@ def main() -> int:
         "bytes_vs_bf16_rmw": {
             "bf16_rmw_bytes_per_step": bf16_rmw_bytes(traffic_shape),
             "ratio_cycle_avg": bf16_rmw_bytes(traffic_shape) / bytes_step,
+            # the reference's ratio: bf16 bytes / its amortised cycle bytes (one
+            # flush per L steps, bench_gdn_replayssm.py:348-353,381)
             "ratio_reference_accounting": bf16_rmw_bytes(traffic_shape)
-            / reference_traffic(traffic_shape, L, args.block_v)["replay_logical"],
+            / reference_traffic(traffic_shape, L, args.block_v)["amortized_actual"],
         },
         "wall_us_per_step": wall * 1e6 / steps,
     }
@@ -362,6 +403,10 @@ def main() -> int:
         }
         log(f"[bench] production-contract bf16 comparator: {packed_us:.3f} us/step, "
             f"ReplaySSM {packed_us / us_step:.2f}x faster")
+    if not args.no_extras and not args.profile:
+        extra = run_extras(EXTRAS, device, stream, buffers=[st["payload"] for st in sets])
+        result.update(extra)
+        result["stream_floor_us"] = extra["stream_floor"]["read_us"]
     if args.cpu_sample > 0 and not args.profile:
         log("[bench] timing the CPU baseline ...")
         result["cpu_baseline"] = cpu_baseline(args, traffic_shape, L)
@@ -372,6 +417,296 @@ def main() -> int:
         calibration_copies(device)
     print(json.dumps(result), flush=True)
     return 0
+
+
+
+# ---------------------------------------------------------------------------
+# Extra measurements: the reference's kernel benchmark (core kernel over a ring
+# cycle, split against fused), BASELINE configs 1 and 3, and the HBM floor.
+# ---------------------------------------------------------------------------
+
+def _graph_us(stream, one_round, calls: int, rounds: int = 3, warm: int = 1) -> float:
+    """Microseconds per launch: one_round() (`calls` launches) run once
+    eagerly, captured in a HIP graph, replayed `warm` + `rounds` times, HIP
+    events on the capture stream around the timed replays."""
+    import torch
+
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        one_round()
+        stream.synchronize()
+        with torch.cuda.graph(graph, stream=stream):
+            one_round()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        for _ in range(warm):
+            graph.replay()
+        start.record(stream)
+        for _ in range(rounds):
+            graph.replay()
+        end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) * 1e3 / (rounds * calls)
+
+
+def _core_sets(B: int, L: int, S: int, device, seed: int) -> list:
+    """S independent (checkpoint, ring) sets at batch B, ring length L: a
+    warm FP8 state (64 recurrence steps) and a full ring of prepared tokens
+    (q/k L2-normalised, gates from the reference's formulas)."""
+    import torch
+
+    import gdn_replayssm_fp8_kernel as gk
+    import gdn_replayssm_synth as synth
+
+    shape = synth.Shape(B)
+    gen = synth.generator(seed, device)
+    a_log, dt_bias = synth.gating_params(shape, gen, device)
+    state = synth.warm_state(shape, 64, gen, device, a_log, dt_bias)
+    ck = gk.quantize_checkpoint(state, saturation=False)
+    del state
+    q, k, v, g, beta = synth.ring_inputs(shape, L, gen, device, a_log, dt_bias)
+    f32 = dict(dtype=torch.float32, device=device)
+    return [dict(payload=ck.payload.clone(), scale=ck.scale.clone(), q=q.clone(), k=k.clone(), v=v.clone(),
+                 g=g.clone(), beta=beta.clone(),
+                 out=torch.empty(B, shape.value_heads, shape.value_dim, dtype=torch.bfloat16, device=device),
+                 tq=torch.empty(B, shape.value_heads, shape.key_dim, **f32),
+                 coef=torch.zeros(B, shape.value_heads, L, **f32)) for _ in range(S)]
+
+
+def _core_launch(st: dict, valid, flush, block_v: int = 128) -> None:
+    import gdn_replayssm_fp8_kernel as gk
+
+    gk.gdn_replay_fp8(st["payload"], st["scale"], st["q"], st["k"], st["v"], st["g"], st["beta"], valid, flush,
+                      block_v=block_v, out=st["out"])
+
+
+def time_core_cycles(device, stream, windows=(4, 8, 16), B: int = 64, S: int = 12) -> dict:
+    """The reference's kernel benchmark cycle (prototype/bench_gdn_replayssm.py
+    :291-330, amortised as :290): the core kernel (gdn_replay_fp8 on prepared
+    rings, no prep) at ring fills 1..L-1, then the flush at fill L, over S
+    rotating sets; us per step over whole cycles, and the replay at fill L-1
+    and the flush alone."""
+    import torch
+
+    res = {}
+    for L in windows:
+        sets = _core_sets(B, L, S, device, seed=300 + L)
+        valid = [torch.full((B,), f, dtype=torch.int32, device=device) for f in range(1, L + 1)]
+        flush = [torch.full((B,), f == L, dtype=torch.bool, device=device) for f in range(1, L + 1)]
+
+        def cycle():
+            for i in range(S * L):
+                c = (i // S) % L
+                _core_launch(sets[i % S], valid[c], flush[c])
+
+        def at_fill(c):
+            def one_round():
+                for i in range(S):
+                    _core_launch(sets[i], valid[c], flush[c])
+            return one_round
+
+        us = _graph_us(stream, cycle, S * L)
+        res[f"L{L}"] = {"us_per_step": round(us, 4),
+                        "replay_us_at_fill_L-1": round(_graph_us(stream, at_fill(L - 2), S), 4) if L > 1 else None,
+                        "flush_us": round(_graph_us(stream, at_fill(L - 1), S), 4)}
+        del sets
+    res["workload"] = (f"core kernel gdn_replay_fp8, B={B}, H=16 HV=32 K=V=128, block_v=128, fills 1..L-1 then the "
+                       f"flush at L, {S} rotating sets, HIP graph")
+    return res
+
+
+def time_config1(device, stream, B: int = 64, L: int = 16, S: int = 12) -> dict:
+    """one core-kernel launch at B=64, L=16 with the ring
+    fills spread uniformly over 1..16 (sequence b at fill b % 16 + 1; the
+    B/16 sequences at 16 flush in the same launch)."""
+    import torch
+
+    sets = _core_sets(B, L, S, device, seed=401)
+    fill = (torch.arange(B, device=device) % L + 1).to(torch.int32)
+    flush = fill == L
+
+    def one_round():
+        for i in range(S):
+            _core_launch(sets[i], fill, flush)
+
+    us = _graph_us(stream, one_round, S)
+    return {"us_per_launch": round(us, 4), "flushing_sequences": int(flush.sum()),
+            "workload": f"core kernel, B={B}, L={L}, fills b % {L} + 1 (flush at {L}) in one launch, {S} rotating sets"}
+
+
+def time_split_vs_fused(device, stream, B: int = 64, L: int = 16, S: int = 12) -> dict:
+    """The reference's tiled-against-split comparison (bench_gdn_replayssm.py
+    :291-330): the replay at fills 1..L-1 as one fused launch (gdn_replay_fp8)
+    and as precompute + apply (gdn_replay_fp8_split), and each cycle with the
+    fused flush at fill L."""
+    import torch
+
+    import gdn_replayssm_fp8_kernel as gk
+
+    sets = _core_sets(B, L, S, device, seed=501)
+    valid = [torch.full((B,), f, dtype=torch.int32, device=device) for f in range(1, L + 1)]
+    no_flush = torch.zeros(B, dtype=torch.bool, device=device)
+    flush = torch.ones(B, dtype=torch.bool, device=device)
+
+    def fused():
+        for i in range(S * (L - 1)):
+            _core_launch(sets[i % S], valid[(i // S) % (L - 1)], no_flush)
+
+    def split():
+        for i in range(S * (L - 1)):
+            st = sets[i % S]
+            gk.gdn_replay_fp8_split(st["payload"], st["scale"], st["q"], st["k"], st["v"], st["g"], st["beta"],
+                                    valid[(i // S) % (L - 1)], st["tq"], st["coef"], block_v=128, out=st["out"])
+
+    def flush_round():
+        for i in range(S):
+            _core_launch(sets[i], valid[L - 1], flush)
+
+    fused_us = _graph_us(stream, fused, S * (L - 1))
+    split_us = _graph_us(stream, split, S * (L - 1))
+    flush_us = _graph_us(stream, flush_round, S)
+    return {"fused_replay_us": round(fused_us, 4), "split_replay_us": round(split_us, 4),
+            "flush_us": round(flush_us, 4),
+            "fused_cycle_us": round(((L - 1) * fused_us + flush_us) / L, 4),
+            "split_cycle_us": round(((L - 1) * split_us + flush_us) / L, 4),
+            "workload": f"B={B}, L={L}, replay fills 1..{L - 1} (cycle average), block_v=128, {S} rotating sets"}
+
+
+def _rel_l2(a, b) -> float:
+    import torch
+
+    return float(torch.linalg.vector_norm((a - b).double()) / torch.linalg.vector_norm(b.double()))
+
+
+def config3(device, stream, windows=(4, 16, 64), B: int = 8, steps: int = 4096,
+            probes=(128, 512, 2048, 4096)) -> dict:
+    """BASELINE config 3 at B=8, L in {4, 16, 64}: the full-contract step
+    (fused prep + replay, flush at fill L) timed over whole ring cycles on
+    enough rotating sets to exceed the Infinity Cache; then, untimed, 4096
+    steps from a zero state with fresh seeded inputs beside an fp32
+    recurrence that consumes the ring values the kernel appended. The state
+    drift follows prototype/qwen35_drift_study.py:355-418: at step s (a flush
+    step) the fp32 replay of the ring on the dequantised checkpoint it started
+    from, against the fp32 state (before the flush requantises); also the
+    requantised checkpoint's own distance."""
+    import torch
+
+    import gdn_replayssm_fp8_kernel as gk
+    import gdn_replayssm_synth as synth
+
+    res = {}
+    shape = synth.Shape(B)
+    HV, K, V, G = shape.value_heads, shape.key_dim, shape.value_dim, shape.group
+    bf = dict(dtype=torch.bfloat16, device=device)
+    for L in windows:
+        # -- timing
+        S = 48
+        gen = synth.generator(600 + L, device)
+        a_log, dt_bias = synth.gating_params(shape, gen, device)
+        state = synth.warm_state(shape, 64, gen, device, a_log, dt_bias)
+        ck = gk.quantize_checkpoint(state, saturation=False)
+        mixed, a_raw, b_raw = synth.raw_step_inputs(shape, L, gen, device)
+        mixed = [mixed[:, t].contiguous() for t in range(L)]
+        a_raw = [a_raw[:, t].contiguous() for t in range(L)]
+        b_raw = [b_raw[:, t].contiguous() for t in range(L)]
+        sets = [dict(payload=ck.payload.clone(), scale=ck.scale.clone(), q_out=torch.zeros(B, shape.heads, K, **bf),
+                     k=torch.zeros(B, L, shape.heads, K, **bf), v=torch.zeros(B, L, HV, V, **bf),
+                     g=torch.zeros(B, L, HV, **bf), beta=torch.zeros(B, L, HV, **bf),
+                     out=torch.empty(B, HV, V, **bf)) for _ in range(S)]
+        fills = [torch.full((B,), f, dtype=torch.int32, device=device) for f in range(1, L + 1)]
+        flushes = [torch.full((B,), f == L, dtype=torch.bool, device=device) for f in range(1, L + 1)]
+
+        def cycle():
+            for i in range(S * L):
+                st, c = sets[i % S], (i // S) % L
+                gk.gdn_prep_replay_fp8(mixed[c], a_raw[c], b_raw[c], a_log, dt_bias, fills[c] - 1, st["payload"],
+                                       st["scale"], st["q_out"], st["k"], st["v"], st["g"], st["beta"], fills[c],
+                                       flushes[c], block_v=128, out=st["out"])
+
+        us = _graph_us(stream, cycle, S * L, rounds=2)
+        del sets, state
+        # -- drift (untimed)
+        gen = synth.generator(700 + L, device)
+        mixed, a_raw, b_raw = synth.raw_step_inputs(shape, steps, gen, device)
+        ck = gk.quantize_checkpoint(torch.zeros(B, HV, V, K, device=device), saturation=False)
+        q_out = torch.zeros(B, shape.heads, K, **bf)
+        k_r, v_r = torch.zeros(B, L, shape.heads, K, **bf), torch.zeros(B, L, HV, V, **bf)
+        g_r, b_r = torch.zeros(B, L, HV, **bf), torch.zeros(B, L, HV, **bf)
+        exact = torch.zeros(B, HV, V, K, device=device)
+
+        def token(S_, t):          # S <- e^g S; S += beta (v - S k) k^T (ref:155-161), fp32
+            k = k_r[:, t].float().repeat_interleave(G, dim=1)
+            S_.mul_(g_r[:, t].float().exp()[..., None, None])
+            r = (S_ * k[:, :, None, :]).sum(-1)
+            S_.add_(((v_r[:, t].float() - r) * b_r[:, t].float()[..., None])[..., None] * k[:, :, None, :])
+
+        drift = {}
+        with torch.no_grad():
+            for step in range(steps):
+                pos = step % L
+                fill = torch.full((B,), pos + 1, dtype=torch.int32, device=device)
+                start = gk.dequantize_checkpoint(ck) if step + 1 in probes else None
+                gk.gdn_prep_replay_fp8(mixed[:, step], a_raw[:, step], b_raw[:, step], a_log, dt_bias, fill - 1,
+                                       ck.payload, ck.scale, q_out, k_r, v_r, g_r, b_r, fill, fill == L)
+                token(exact, pos)
+                if start is not None:
+                    for t in range(L):
+                        token(start, t)
+                    drift[str(step + 1)] = {"state": round(_rel_l2(start, exact), 6),
+                                            "checkpoint": round(_rel_l2(gk.dequantize_checkpoint(ck), exact), 6)}
+        res[f"L{L}"] = {"us_per_step": round(us, 4), "drift": drift}
+        del mixed, a_raw, b_raw, exact
+    res["workload"] = (f"full-contract step (fused prep + replay, flush at L), B={B}, H=16 HV=32 K=V=128, "
+                       f"timed over whole cycles on 48 rotating sets; drift over {steps} steps from a zero state")
+    return res
+
+
+def stream_floor(device, stream, buffers: list) -> dict:
+    """The HBM floor of the checkpoint traffic at the bench's buffer rotation:
+    one coalesced pass over each set's codes in turn (gdnr_stream_probe), read
+    only (what a replay must read) and read + written back in place (what a
+    flush must move)."""
+    import gdnr_lib
+
+    def probe(write):
+        def one_round():
+            for buf in buffers:
+                gdnr_lib.call("gdnr_stream_probe", [buf], [write], gdnr_lib.current_stream(device))
+        return one_round
+
+    n = len(buffers)
+    nbytes = buffers[0].numel() * buffers[0].element_size()
+    read_us = _graph_us(stream, probe(0), n, rounds=5)
+    rw_us = _graph_us(stream, probe(1), n, rounds=5)
+    return {"read_us": round(read_us, 4), "read_write_us": round(rw_us, 4), "bytes": nbytes,
+            "read_GBps": round(nbytes / (read_us * 1e-6) / 1e9, 1),
+            "read_write_GBps": round(2 * nbytes / (rw_us * 1e-6) / 1e9, 1),
+            "workload": f"{n} rotating checkpoint code buffers of {nbytes} bytes, one coalesced pass each"}
+
+
+def run_extras(names, device, stream, buffers=None) -> dict:
+    """The extra measurements by name (EXTRAS); buffers: the checkpoint code
+    tensors of the headline's sets for the stream floor (fresh ones if None)."""
+    import torch
+
+    out = {}
+    for name in names:
+        t0 = time.perf_counter()
+        if name == "core":
+            out["core_cycle"] = time_core_cycles(device, stream)
+        elif name == "config1":
+            out["config1_single_launch"] = time_config1(device, stream)
+        elif name == "split":
+            out["split_vs_fused"] = time_split_vs_fused(device, stream)
+        elif name == "config3":
+            out["config3"] = config3(device, stream)
+        elif name == "floor":
+            if buffers is None:
+                buffers = [torch.zeros(64, 32, 128, 128, dtype=torch.uint8, device=device) for _ in range(12)]
+            out["stream_floor"] = stream_floor(device, stream, buffers)
+        log(f"[bench] extra '{name}' done in {time.perf_counter() - t0:.1f} s")
+    return out
 
 
 def time_slot_path(args, shape, device, stream, ck, mixed, a_raw, b_raw, a_log, dt_bias, meta, rounds,

@@ -935,6 +935,26 @@ int gdnr_dequantize_vblock32(const gdnr_tensor* payload, const gdnr_tensor* scal
   return hip_status(gdnr::launch_dequantize(q, stream));
 }
 
+int gdnr_stream_probe(const gdnr_tensor* buffer, int32_t write, void* stream) {
+  g_last_error.clear();
+  if (!buffer) return fail(GDNR_ERR_INVALID_ARGUMENT, "buffer: null tensor descriptor");
+  if (buffer->ndim < 1 || buffer->ndim > GDNR_MAX_DIMS)
+    return fail(GDNR_ERR_INVALID_ARGUMENT, "buffer: %d dims", buffer->ndim);
+  GDNR_TRY(check_desc(buffer, "buffer", buffer->ndim));
+  // C-contiguous, whole 16-byte pieces
+  int64_t numel = 1;
+  for (int d = buffer->ndim - 1; d >= 0; --d) {
+    if (buffer->shape[d] > 1 && buffer->strides[d] != numel)
+      return fail(GDNR_ERR_INVALID_ARGUMENT, "buffer: not contiguous (dim %d)", d);
+    numel *= buffer->shape[d];
+  }
+  const int64_t bytes = numel * elem_size(buffer->dtype);
+  if (bytes % 16) return fail(GDNR_ERR_INVALID_ARGUMENT, "buffer: %lld bytes is not a multiple of 16", (long long)bytes);
+  GDNR_TRY(check_align(buffer, "buffer", 16));
+  if (bytes == 0) return GDNR_OK;
+  return hip_status(gdnr::launch_stream_probe(buffer->data, bytes, write != 0, stream));
+}
+
 int gdnr_bf16_step(const gdnr_tensor* state, const gdnr_tensor* q, const gdnr_tensor* k, const gdnr_tensor* v,
                    const gdnr_tensor* g, const gdnr_tensor* beta, const gdnr_tensor* out, void* stream) {
   g_last_error.clear();

@@ -104,12 +104,16 @@ def reference_traffic(s: LayerShape, window: int, block_v: int) -> dict:
     ring_key = s.batch * window * s.heads * s.key_dim * 2
     ring_value = s.batch * window * s.value_heads * s.value_dim * 2
     ring_scalars = s.batch * window * s.value_heads * 4
-    return {
+    out = {
         "replay_logical": checkpoint + scales + query + ring_key + ring_value + ring_scalars,
         "replay_actual": checkpoint + scales + tiles * (query + ring_key) + ring_value + ring_scalars,
         "flush_actual": 2 * checkpoint + 2 * scales + tiles * ring_key + ring_value + ring_scalars,
         "bf16_baseline": bf16_rmw_bytes(s),
     }
+    # one ring cycle: L - 1 replays and one flush (bench_gdn_replayssm.py:348-353)
+    out["amortized_actual"] = (out["replay_actual"] * (window - 1) + out["flush_actual"]) / window
+    out["amortized_logical"] = (out["replay_logical"] * (window - 1) + out["flush_actual"]) / window
+    return out
 
 
 # ---------------------------------------------------------------------------

@@ -34,7 +34,7 @@ DEVICE_FLAGS = [
 HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra"]
 ACTS = ("bf16", "f16", "f32")  # activation dtypes, one kernel object each (GDNR_ACT = index)
 KERNEL_SOURCES = ("gdnr_kernels", "gdnr_step", "gdnr_decode")  # compiled once per activation dtype
-SINGLE_SOURCES = ("gdnr_rmw", "gdnr_formats", "gdnr_status")  # compiled once (dtypes are template arguments)
+SINGLE_SOURCES = ("gdnr_rmw", "gdnr_formats", "gdnr_status", "gdnr_probe")  # compiled once (dtypes are template arguments)
 # per-source device flags: the decode kernel's first 13 argument dwords are
 # preloaded into SGPRs at wave launch (gfx950 kernarg preload), and its
 # wave-uniform branches (workgroup role, replay or flush) are left as scalar

@@ -70,6 +70,7 @@ ENTRY_POINTS = {
     "gdnr_bf16_step_packed": (8, 0, 1),
     "gdnr_quantize_checkpoint": (4, 2),
     "gdnr_dequantize_checkpoint": (3, 2),
+    "gdnr_stream_probe": (1, 1),
 }
 
 _lib = None

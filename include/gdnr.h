@@ -79,15 +79,30 @@ int gdnr_abi_version(void);
 
 /*
  * Diagnostics of the decode kernels' bounded waits. Inside a workgroup the
- * waves of a value head hand the coefficient chain to each other through an
- * LDS flag, and every such wait is bounded (2^22 polls). A wait that gives
- * up adds 1 to a per-device status word and the workgroup skips its
- * in-place checkpoint and scale stores (its output is then meaningless).
+ * waves hand the coefficient chain, the flush factors and the flush's
+ * helper results to each other through LDS flags, and every such wait is
+ * bounded (2^22 polls). A wait that gives up adds 1 to a per-device status
+ * word; the wave then goes on with whatever the LDS holds (the step kernel
+ * skips its in-place checkpoint and scale stores), so its outputs are
+ * meaningless.
  * *count receives the current device's word; reset != 0 clears it. This
  * call synchronises the device (it copies the word to the host).
  * No counterpart in the reference (its Triton kernels have no inter-wave waits).
  */
 int gdnr_wait_timeouts(uint32_t* count, int32_t reset);
+
+/*
+ * Measurement probe: one coalesced pass over `buffer` (any dtype,
+ * C-contiguous, 16-byte aligned, a whole number of 16-byte pieces), reading
+ * it (write == 0) or reading it and writing every piece back unchanged in
+ * place (write != 0). Timed by the benchmark as the HBM floor of the decode
+ * step's checkpoint traffic (the replay reads the codes once, the flush
+ * reads and rewrites them). The buffer's contents are left unchanged.
+ * No counterpart in the reference (its byte counts are formulas:
+ * prototype/bench_gdn_replayssm.py:45-87; its bandwidth probes are
+ * prototype/bench_kernel_diag.py:39-148).
+ */
+int gdnr_stream_probe(const gdnr_tensor* buffer, int32_t write, void* stream);
 
 /*
  * One decode step of the replay, per sequence b:
@@ -223,7 +238,10 @@ int gdnr_prep_replay_fp8_slots(const gdnr_tensor* mixed_qkv, const gdnr_tensor* 
 
 /*
  * vblock32 quantiser, bit-exact with the reference's
- *   scale = fp16(amax/448) if amax > 0 else 1;  codes = e4m3fn(clamp(x/scale, +-448))
+ *   s = amax/448 (f32) if amax > 0 else 1;  codes = e4m3fn(clamp(x/s, +-448));
+ *   stored scale = fp16(s)
+ * (the codes divide by the unrounded f32 s, as the reference does before it
+ * stores the scale in fp16: ref:83-99).
  * state [B,HV,V,K] f32 -> payload [B,HV,V,K] fp8|u8, scale [B,HV,V/32] f16|f32.
  * saturated (optional, may be NULL) [B,HV,V/32] i32 receives the per-vblock
  * count of |x/scale| > 448.
