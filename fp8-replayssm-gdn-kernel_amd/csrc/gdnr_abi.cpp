@@ -340,7 +340,7 @@ gdnr::StepArgs make_step_args(const gdnr::ReplayArgs& r, int es, int gate_es) {
   s.al_s = u32(4 * r.al_s), s.db_s = u32(4 * r.db_s);
   s.qo_b = u32(es * r.qo_b), s.qo_h = u32(es * r.qo_h);
   s.B = r.B, s.H = r.H, s.G = r.G, s.V = r.V, s.L = r.L, s.gw = r.gw, s.block_v = r.block_v, s.n_vt = r.n_vt;
-  s.sw = r.sw, s.rpw = r.rpw, s.units = r.units;
+  s.sw = r.sw, s.rpw = r.rpw, s.units = r.units, s.nwh = r.nwh;
   s.out_scale = r.out_scale;
   s.lds_q = r.lds_q, s.lds_knew = r.lds_knew, s.lds_k = r.lds_k, s.lds_flag = r.lds_flag, s.lds_c = r.lds_c;
   s.lds_t = r.lds_t, s.lds_g = r.lds_g, s.lds_v = r.lds_v, s.lds_r = r.lds_r, s.lds_fac = r.lds_fac;
@@ -436,24 +436,31 @@ bool decode_eligible(const gdnr::ReplayArgs& a, int act) {
          (a.V == 64 || a.V == 128 || a.V == 256);
 }
 void fit_decode(gdnr::ReplayArgs* a) {
-  const int32_t nwh = a->V == 256 ? 2 : 1;  // row waves per value head
+  const int32_t cus = gdnr::device_cus();
+  a->nwh = a->V == 256 ? 2 : 1;  // row waves per value head
   a->gw = a->G % 2 == 0 ? 2 : 1;  // value heads per unit (at most 2; they share the unit's chain wave)
+  // small batches: one value head per unit (twice the units), and for V = 128
+  // two row waves of 64 rows per head while the units do not outnumber the
+  // compute units: the launch spreads over the whole chip, and every wave's
+  // share of the stream (and of a flush) is short
+  if (a->gw == 2 && (int64_t)a->B * a->H * (a->G / 2) < cus) a->gw = 1;
+  if (a->V == 128 && (int64_t)a->B * a->H * (a->G / a->gw) <= cus) a->nwh = 2;
   a->sw = a->V / 64;
   // units per workgroup: as many as fit one CU (12 waves) while the grid
   // still covers every CU; the kernel takes a workgroup's units as SP
   // sequences x HP head groups (4 = 2 x 2, 2 = 2 x 1), which must divide B
   // and the head groups of a sequence
-  const int32_t per_seq = a->H * (a->G / a->gw), waves = 1 + a->gw * nwh;
+  const int32_t per_seq = a->H * (a->G / a->gw), waves = 1 + a->gw * a->nwh;
   a->units = 1;
   for (int32_t u : {4, 2}) {
     const int32_t hp = u == 4 ? 2 : 1, sp = u / hp;
-    if (a->B % sp == 0 && per_seq % hp == 0 && u * waves <= 12 &&
-        (int64_t)a->B * per_seq / u >= gdnr::device_cus()) {
+    if (a->B % sp == 0 && per_seq % hp == 0 && u * waves <= 12 && (int64_t)a->B * per_seq / u >= cus) {
       a->units = u;
       break;
     }
   }
-  a->lds_bytes = gdnr::decode_lds_bytes(a->units, a->gw * nwh, a->V == 64 ? 2 : 4);
+  // vblocks per row wave: V / 32 / nwh
+  a->lds_bytes = gdnr::decode_lds_bytes(a->units, a->gw * a->nwh, a->V / 32 / a->nwh);
 }
 int launch_decode(const gdnr::ReplayArgs& r, int act, bool fused, bool gate_f32, void* stream) {
   gdnr::StepArgs a = make_step_args(r, elem_size(act), gate_f32 ? 4 : elem_size(act));

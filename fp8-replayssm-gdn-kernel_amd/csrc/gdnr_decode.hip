@@ -1155,8 +1155,10 @@ int32_t decode_lds_bytes(int32_t units, int32_t row_waves, int32_t vblocks) {
 int GDNR_SUFFIX(launch_decode)(const StepArgs& a, bool fused, bool gate_f32, void* stream) {
   hipStream_t s = (hipStream_t)stream;
   int rc;
-  // V = 64 a.sw: one wave of 64 rows per value head; 128: one of 128 rows; 256: two
+  // V = 64 a.sw: one wave of 64 rows per value head; 128: one of 128 rows,
+  // or two of 64 (small batches); 256: two of 128
   if (a.sw == 1) rc = launch_shape<4, 1>(a, fused, gate_f32, s);
+  else if (a.sw == 2 && a.nwh == 2) rc = launch_shape<4, 2>(a, fused, gate_f32, s);
   else if (a.sw == 2) rc = launch_shape<8, 1>(a, fused, gate_f32, s);
   else rc = launch_shape<8, 2>(a, fused, gate_f32, s);
   if (rc) return rc;
