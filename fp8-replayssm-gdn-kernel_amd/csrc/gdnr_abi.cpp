@@ -305,6 +305,35 @@ bool step_offsets_fit(const gdnr::ReplayArgs& a, int es) {
   return ok;
 }
 
+// The decode kernel forms each sequence's (slot's) base address in 64 bits
+// and every offset inside one sequence, or inside the per-batch tensors, in
+// 32 bits: it takes checkpoints and rings of any total size whose sequence
+// strides fit 32 bits and whose per-sequence extent is below 2^31 bytes.
+bool decode_offsets_fit(const gdnr::ReplayArgs& a, int es) {
+  const int64_t lim = (int64_t)1 << 31, ulim = (int64_t)1 << 32;
+  const int64_t B = a.B, L = a.L, HV = a.HV, H = a.H, V = a.V, K = gdnr::kKeyDim;
+  auto fits = [lim](int64_t extent_bytes) { return extent_bytes >= 0 && extent_bytes < lim; };
+  auto stride_fits = [ulim](int64_t stride_bytes) { return stride_bytes >= 0 && stride_bytes < ulim; };
+  bool ok = stride_fits(a.ck_b) && stride_fits(2 * a.sc_b) && stride_fits(es * a.k_b) && stride_fits(es * a.v_b) &&
+            stride_fits(es * a.g_b) && stride_fits(es * a.be_b) &&
+            fits((HV - 1) * a.ck_h + (V - 1) * a.ck_v + K) &&
+            fits(2 * ((HV - 1) * a.sc_h + (V / gdnr::kVBlock - 1) * a.sc_v + 1)) &&
+            fits(es * ((L - 1) * a.k_t + (H - 1) * a.k_h + K)) && fits(es * ((L - 1) * a.v_t + (HV - 1) * a.v_h + V)) &&
+            fits(es * ((L - 1) * a.g_t + (HV - 1) * a.g_h + 1)) && fits(es * ((L - 1) * a.be_t + (HV - 1) * a.be_h + 1)) &&
+            (!a.slot || fits(4 * ((B - 1) * a.sl_s + 1))) &&
+            fits(es * ((B - 1) * a.o_b + (HV - 1) * a.o_h + V)) && fits(4 * ((B - 1) * a.vl_s + 1)) &&
+            fits((B - 1) * a.fl_s + 4);
+  if (a.mixed) {
+    ok = ok && fits(es * ((B - 1) * a.mx_b + 2 * H * K + HV * V)) && fits(4 * ((B - 1) * a.pos_s + 1)) &&
+         fits(es * ((B - 1) * a.qo_b + (H - 1) * a.qo_h + K)) && fits(4 * ((B - 1) * a.a_b + (HV - 1) * a.a_h + 1)) &&
+         fits(4 * ((B - 1) * a.bg_b + (HV - 1) * a.bg_h + 1)) && fits(4 * ((HV - 1) * a.al_s + 1)) &&
+         fits(4 * ((HV - 1) * a.db_s + 1));
+  } else {
+    ok = ok && fits(es * ((B - 1) * a.q_b + (H - 1) * a.q_h + K));
+  }
+  return ok;
+}
+
 // StepArgs from a validated, fitted ReplayArgs (element strides -> byte strides).
 gdnr::StepArgs make_step_args(const gdnr::ReplayArgs& r, int es, int gate_es) {
   gdnr::StepArgs s = {};
@@ -632,11 +661,11 @@ int gdnr_replay_fp8(const gdnr_tensor* checkpoint, const gdnr_tensor* checkpoint
   a.out = out->data;
   a.o_b = out->strides[0];
   a.o_h = out->strides[1];
+  if (a.L <= gdnr::kStepRing && decode_eligible(a, g.act) && decode_offsets_fit(a, elem_size(g.act))) {
+    fit_decode(&a);
+    return hip_status(launch_decode(a, g.act, false, false, stream));
+  }
   if (a.L <= gdnr::kStepRing && step_offsets_fit(a, elem_size(g.act))) {
-    if (decode_eligible(a, g.act)) {
-      fit_decode(&a);
-      return hip_status(launch_decode(a, g.act, false, false, stream));
-    }
     GDNR_TRY(fit_step(&a, elem_size(g.act)));
     return hip_status(launch_step(a, g.act, false, false, stream));
   }
@@ -845,11 +874,11 @@ int gdnr_prep_replay_fp8(const gdnr_tensor* mixed_qkv, const gdnr_tensor* a, con
   r.out = out->data;
   r.o_b = out->strides[0];
   r.o_h = out->strides[1];
+  if (r.L <= gdnr::kStepRing && decode_eligible(r, g.act) && decode_offsets_fit(r, elem_size(g.act))) {
+    fit_decode(&r);
+    return hip_status(launch_decode(r, g.act, true, a->dtype == GDNR_DTYPE_F32, stream));
+  }
   if (r.L <= gdnr::kStepRing && step_offsets_fit(r, elem_size(g.act))) {
-    if (decode_eligible(r, g.act)) {
-      fit_decode(&r);
-      return hip_status(launch_decode(r, g.act, true, a->dtype == GDNR_DTYPE_F32, stream));
-    }
     GDNR_TRY(fit_step(&r, elem_size(g.act)));
     return hip_status(launch_step(r, g.act, true, a->dtype == GDNR_DTYPE_F32, stream));
   }
@@ -899,12 +928,16 @@ int gdnr_prep_replay_fp8_slots(const gdnr_tensor* mixed_qkv, const gdnr_tensor* 
   r.out = out->data;
   r.o_b = out->strides[0];
   r.o_h = out->strides[1];
-  if (!step_offsets_fit(r, elem_size(g.act)))
-    return fail(GDNR_ERR_UNSUPPORTED, "state_indices: the slot tensors must span less than 2 GiB each");
   if (decode_eligible(r, g.act)) {
+    if (!decode_offsets_fit(r, elem_size(g.act)))
+      return fail(GDNR_ERR_UNSUPPORTED,
+                  "state_indices: a slot's checkpoint and ring rows must span less than 2 GiB, and the slot "
+                  "strides 4 GiB");
     fit_decode(&r);
     return hip_status(launch_decode(r, g.act, true, a->dtype == GDNR_DTYPE_F32, stream));
   }
+  if (!step_offsets_fit(r, elem_size(g.act)))
+    return fail(GDNR_ERR_UNSUPPORTED, "state_indices: the slot tensors must span less than 2 GiB each");
   GDNR_TRY(fit_step(&r, elem_size(g.act)));
   return hip_status(launch_step(r, g.act, true, a->dtype == GDNR_DTYPE_F32, stream));
 }

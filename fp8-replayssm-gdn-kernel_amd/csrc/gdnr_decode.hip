@@ -143,6 +143,11 @@ __device__ __forceinline__ const StepArgs& opaque_args() {
   return *(const StepArgs*)(c_args*)(((uint64_t)hi << 32) | lo);
 }
 __device__ __forceinline__ uint32_t ld32(const uint8_t* p) { return *(const uint32_t*)p; }
+// A sequence's (slot's) base in a tensor, in 64 bits: the tensors of a slot
+// cache may span more than 4 GiB; offsets inside one sequence stay 32-bit.
+__device__ __forceinline__ uint8_t* sbase(const uint8_t* p, int seq, uint32_t stride) {
+  return (uint8_t*)p + (uint64_t)(uint32_t)seq * stride;
+}
 // Direct global -> LDS copy of 16 bytes per lane (global_load_lds_dwordx4):
 // lane l's 16 bytes land at LDS address lds_addr + 16 l (lds_addr wave-uniform,
 // through M0, which is restored). Written as inline assembly so that the
@@ -555,7 +560,7 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
     // the fill are zeroed below), the metadata, the query / new-token rows,
     // the gates (lane (t, j): token t of head j)
     const int tl = l16 < L ? l16 : 0;
-    const uint8_t* krow = kring + (bs * k_b + h * k_h + (uint32_t)tl * k_t) + 64 * q4;
+    const uint8_t* krow = sbase(kring, bs, k_b) + (h * k_h + (uint32_t)tl * k_t) + 64 * q4;
     u32x4_t xr[4];
 #pragma unroll
     for (int m = 0; m < 4; ++m) xr[m] = ld16(krow + 16 * m);
@@ -571,8 +576,8 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
     } else {
       qbits = ld32(a.q + (b * a.q_b + h * a.q_h) + 4 * lane);
     }
-    const uint32_t g_raw = *(const uint16_t*)(a.g + (bs * a.g_b + (uint32_t)tl * a.g_t + hvr * a.g_h));
-    const uint32_t be_raw = *(const uint16_t*)(a.beta + (bs * a.be_b + (uint32_t)tl * a.be_t + hvr * a.be_h));
+    const uint32_t g_raw = *(const uint16_t*)(sbase(a.g, bs, a.g_b) + ((uint32_t)tl * a.g_t + hvr * a.g_h));
+    const uint32_t be_raw = *(const uint16_t*)(sbase(a.beta, bs, a.be_b) + ((uint32_t)tl * a.be_t + hvr * a.be_h));
     uint32_t ab0 = 0, ab1 = 0;
     float alog = 0.f, dtb = 0.f;
     if constexpr (FUSED) {
@@ -632,7 +637,7 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
       }
     }
     auto job_rows = [&](int wv) {
-      return ckpt + (h_bs * ck_b + (hv0 + wv / NWH) * ck_h + RPW * (wv % NWH) * ck_v);
+      return sbase(ckpt, h_bs, ck_b) + ((hv0 + wv / NWH) * ck_h + RPW * (wv % NWH) * ck_v);
     };
     auto job_buf = [&](int kk, int wv) {
       const int bu = kk == 0 ? hv_unit : (hv_unit == u ? up : u);
@@ -654,7 +659,7 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
         // q_out and the ring append of the new key (one unit per key head)
         if (grp == 0) {
           *(uint32_t*)(a.q_out + (b * a.qo_b + h * a.qo_h) + 4 * lane) = qw;
-          if (pos >= 0) *(uint32_t*)(kring + (bs * k_b + (uint32_t)pos * k_t + h * k_h) + 4 * lane) = kw;
+          if (pos >= 0) *(uint32_t*)(sbase(kring, bs, k_b) + ((uint32_t)pos * k_t + h * k_h) + 4 * lane) = kw;
         }
       } else {
         qw = qbits;
@@ -738,8 +743,8 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
       const float gate_new = Act::round(-expf(alog) * sp);
       const float beta_new = Act::round(1.0f / (1.0f + expf(-b_in)));
       if (pos >= 0 && l16 == 0 && pub) {
-        *(uint16_t*)(a.g + (bs * a.g_b + (uint32_t)pos * a.g_t + hvr * a.g_h)) = (uint16_t)act_bits(gate_new);
-        *(uint16_t*)(a.beta + (bs * a.be_b + (uint32_t)pos * a.be_t + hvr * a.be_h)) = (uint16_t)act_bits(beta_new);
+        *(uint16_t*)(sbase(a.g, bs, a.g_b) + ((uint32_t)pos * a.g_t + hvr * a.g_h)) = (uint16_t)act_bits(gate_new);
+        *(uint16_t*)(sbase(a.beta, bs, a.be_b) + ((uint32_t)pos * a.be_t + hvr * a.be_h)) = (uint16_t)act_bits(beta_new);
       }
       gg = l16 == pos ? gate_new : gg;
       bb = l16 == pos ? beta_new : bb;
@@ -886,7 +891,7 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
         for (int k = 0; k < 4; ++k) c[k >> 1][k & 1] = *(const u32x4_t*)(buf + 1024 * k + 16 * lane);
         const int hvj = hv0 + wv / NWH, partj = wv % NWH;
         uint8_t* const sc_j =
-            a.scale + (h_bs * a.sc_b + hvj * a.sc_h + (RPW * partj / kVBlock + pv) * a.sc_v);
+            sbase(a.scale, h_bs, a.sc_b) + (hvj * a.sc_h + (RPW * partj / kVBlock + pv) * a.sc_v);
         const float scp = f16_bits_to_f32(ld_u16_uniform(sc_j));
         const uint8_t* hbv = uv + kLHeads + (wv / NWH) * kHeadLds;
         float op[2];
@@ -920,7 +925,7 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
   // the other tiles only for the replay (the flush reads each vblock in turn,
   // and a wave with fewer loads in the memory pipeline gets to its first
   // vblock sooner)
-  uint8_t* ck_rows = ckpt + (bs * ck_b + hv * ck_h + R0 * ck_v);
+  uint8_t* ck_rows = sbase(ckpt, bs, ck_b) + (hv * ck_h + R0 * ck_v);
   u32x4_t cw[TPW][2];
   auto load_tile = [&](int i) {
     const uint32_t off = (uint32_t)(32 * (i >> 1) + 2 * l16 + (i & 1)) * ck_v + 32 * q4;
@@ -945,7 +950,7 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
     const int nhelp = has_partner ? (partner_flushes(A) ? 0 : 2) : 1;
     nh = uni(helper_vblocks(VB, rpu, nhelp));
   }
-  uint8_t* scale_hv = A.scale + (bs * A.sc_b + hv * A.sc_h);
+  uint8_t* scale_hv = sbase(A.scale, bs, A.sc_b) + (hv * A.sc_h);
   const int vb0 = R0 / kVBlock;
   float sct[VB];  // the vblock scales
 #pragma unroll
@@ -961,7 +966,7 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
   auto vtok = [&](int k) { return k * TPL + lane / CPT; };
   u32x4_t vq[NVL];
   {
-    const uint8_t* vbase = A.v + (bs * A.v_b + hv * A.v_h + R0 * ES) + 16 * vpiece;
+    const uint8_t* vbase = sbase(A.v, bs, A.v_b) + (hv * A.v_h + R0 * ES) + 16 * vpiece;
 #pragma unroll
     for (int k = 0; k < NVL; ++k) {
       const int t = vtok(k);
@@ -983,7 +988,7 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
   // starts, so its waits for each vblock's codes never cover a store.)
   if constexpr (FUSED) {
     if (pos >= 0 && !do_flush) {
-      uint8_t* vw = A.v + (bs * A.v_b + (uint32_t)pos * A.v_t + hv * A.v_h + R0 * ES) + 16 * vpiece;
+      uint8_t* vw = sbase(A.v, bs, A.v_b) + ((uint32_t)pos * A.v_t + hv * A.v_h + R0 * ES) + 16 * vpiece;
 #pragma unroll
       for (int k = 0; k < NVL; ++k)
         if (vtok(k) == pos) *(u32x4_t*)vw = vq[k];
@@ -1111,7 +1116,7 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
   if (lane < own) *(uint16_t*)(scale_hv + (vb0 + lane) * A.sc_v) = (uint16_t)new_scale;
   if constexpr (FUSED) {
     if (pos >= 0 && lane < CPT) {
-      uint8_t* vw = A.v + (bs * A.v_b + (uint32_t)pos * A.v_t + hv * A.v_h + R0 * ES) + 16 * lane;
+      uint8_t* vw = sbase(A.v, bs, A.v_b) + ((uint32_t)pos * A.v_t + hv * A.v_h + R0 * ES) + 16 * lane;
       *(u32x4_t*)vw = *(const u32x4_t*)(vl + pos * VSTRIDE + 16 * lane);
     }
   }

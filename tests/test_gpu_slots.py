@@ -91,6 +91,51 @@ def test_slots_equal_direct_path(device):
         assert torch.equal(r[0], before)
 
 
+def test_slots_beyond_4096_equal_direct_path(device):
+    """A cache of 5000 slots (a 2.6 GB checkpoint, more than 4 GiB of ring and
+    checkpoint together: every sequence's base address needs 64 bits): six
+    sequences in slots 4999, 4097, 4096, 2049, 4998 and 17, 10 steps with
+    staggered fills (L=8, so some flush): outputs, ring rows and checkpoint
+    bytes equal the direct path's on batch-ordered copies, bit for bit."""
+    L, B, steps, n_slots = 8, 6, 10, 5000
+    shape = synth.Shape(B)
+    gen = synth.generator(63, device)
+    a_log, dt_bias = synth.gating_params(shape, gen, device)
+    state = synth.warm_state(shape, 16, gen, device, a_log, dt_bias)
+    ck = gk.quantize_checkpoint(state)
+    slot_of = [4999, 4097, 4096, 2049, 4998, 17]
+    cache = ReplaySSMCache(n_slots, L, device=device)
+    for i, sl in enumerate(slot_of):
+        cache.payload[sl].copy_(ck.payload[i])
+        cache.scale[sl].copy_(ck.scale[i])
+        cache.fill[sl] = (3 * i) % L
+    direct = dict(payload=ck.payload.clone(), scale=ck.scale.clone(),
+                  rings=[torch.zeros(B, L, 16, 128, dtype=torch.bfloat16, device=device),
+                         torch.zeros(B, L, 32, 128, dtype=torch.bfloat16, device=device),
+                         torch.zeros(B, L, 32, dtype=torch.bfloat16, device=device),
+                         torch.zeros(B, L, 32, dtype=torch.bfloat16, device=device)])
+    fill = np.array([(3 * i) % L for i in range(B)])
+    mixed, a, b = synth.raw_step_inputs(shape, steps, gen, device)
+    flushed = 0
+    for step in range(steps):
+        got = cache.step(slot_of, mixed[:, step].contiguous(), a[:, step].contiguous(), b[:, step].contiguous(),
+                         a_log, dt_bias)
+        valid = torch.as_tensor(fill + 1, dtype=torch.int32, device=device)
+        flushed += int((fill + 1 == L).sum())
+        q_out = torch.empty(B, 16, 128, dtype=torch.bfloat16, device=device)
+        want = gk.gdn_prep_replay_fp8(mixed[:, step].contiguous(), a[:, step].contiguous(), b[:, step].contiguous(),
+                                      a_log, dt_bias, valid - 1, direct["payload"], direct["scale"], q_out,
+                                      *direct["rings"], valid, valid == L)
+        fill = np.where(fill + 1 == L, 0, fill + 1)
+        assert torch.equal(got, want), step
+    assert flushed >= B
+    for i, sl in enumerate(slot_of):
+        assert torch.equal(cache.payload[sl].view(torch.uint8), direct["payload"][i].view(torch.uint8)), sl
+        assert torch.equal(cache.scale[sl], direct["scale"][i]), sl
+        for r_cache, r_direct in zip((cache.k_ring, cache.v_ring, cache.g_ring, cache.beta_ring), direct["rings"]):
+            assert torch.equal(r_cache[sl], r_direct[i]), sl
+
+
 def test_cache_lifecycle_matches_oracle(device):
     """Three sequences in a 4-slot cache, L=4: A starts at step 0, B at step 2,
     C replaces A in A's slot at step 7 (A released). Each sequence's outputs
