@@ -533,8 +533,8 @@ int check_prep_inputs(const gdnr_tensor* mixed_qkv, const gdnr_tensor* a, const 
     return fail(GDNR_ERR_INVALID_ARGUMENT, "mixed_qkv: dtype %s differs from the ring dtype %s",
                 dtype_name(mixed_qkv->dtype), dtype_name(g.act));
   const int64_t width = 2 * g.H * g.K + g.HV * g.V;
-  if (mixed_qkv->shape[0] != g.B || mixed_qkv->shape[1] < width)
-    return fail(GDNR_ERR_INVALID_ARGUMENT, "mixed_qkv: shape [%lld, %lld], expected [%lld, >= %lld]",
+  if (mixed_qkv->shape[0] != g.B || mixed_qkv->shape[1] != width)
+    return fail(GDNR_ERR_INVALID_ARGUMENT, "mixed_qkv: shape [%lld, %lld], expected [%lld, %lld] (2 H K + HV V)",
                 (long long)mixed_qkv->shape[0], (long long)mixed_qkv->shape[1], (long long)g.B, (long long)width);
   GDNR_TRY(check_inner_unit(mixed_qkv, "mixed_qkv"));
   GDNR_TRY(check_align(mixed_qkv, "mixed_qkv", 2 * elem_size(g.act)));

@@ -53,6 +53,24 @@ def _check_record(layer, record) -> None:
     state = record["state"]
     if state is not None and (state.dim() != 4 or state.shape[0] != 1 or state.shape[1] != hv):
         raise CaptureFormatError(f"layer {layer}: state must be [1, {hv}, V, K]")
+    # the fused step applies an in-kernel q/k L2 norm and the output scale
+    # K^-1/2 (kernel:534-562, ref:166-186); a record made otherwise runs other
+    # maths than its production_out
+    if record["use_qk_l2norm_in_kernel"] is not True:
+        raise CaptureFormatError(f"layer {layer}: use_qk_l2norm_in_kernel must be true (the step normalises q/k)")
+    if state is not None:
+        V, K = state.shape[2], state.shape[3]
+        if abs(float(record["scale"]) - K ** -0.5) > 1e-6 * K ** -0.5:
+            raise CaptureFormatError(f"layer {layer}: scale {record['scale']} is not K^-1/2 = {K ** -0.5} (K={K})")
+        width = record["mixed_qkv"][0].shape[1] if steps else 0
+        qk = width - hv * V
+        if steps and (qk <= 0 or qk % (2 * K) or hv % (qk // (2 * K))):
+            raise CaptureFormatError(f"layer {layer}: mixed_qkv width {width} is not 2 H K + HV V with K={K}, "
+                                     f"HV={hv}, V={V} and H dividing HV")
+        if any(t.shape[1] != width for t in record["mixed_qkv"]):
+            raise CaptureFormatError(f"layer {layer}: mixed_qkv entries differ in width")
+        if any(t.shape[1] != hv * V for t in record["production_out"]):
+            raise CaptureFormatError(f"layer {layer}: production_out entries must be [1, HV V] = [1, {hv * V}]")
 
 
 def load_capture(path: str | Path) -> dict:

@@ -55,6 +55,12 @@ def test_round_trip_and_replication(tmp_path):
     (lambda r: r["a"].pop(), "list of"),
     (lambda r: r.__setitem__("state", torch.zeros(1, HV + 1, V, K)), "state"),
     (lambda r: r["b"].__setitem__(0, torch.zeros(1, HV + 2)), "b entries"),
+    (lambda r: r.__setitem__("use_qk_l2norm_in_kernel", False), "use_qk_l2norm_in_kernel"),
+    (lambda r: r.__setitem__("scale", 1.0), "K\\^-1/2"),
+    (lambda r: r.__setitem__("mixed_qkv", [torch.zeros(1, 2 * H * K + HV * V + 64) for _ in range(T)]), "mixed_qkv width"),
+    (lambda r: r.__setitem__("mixed_qkv", [torch.zeros(1, 2 * 3 * K + HV * V) for _ in range(T)]), "mixed_qkv width"),
+    (lambda r: r["mixed_qkv"].__setitem__(2, torch.zeros(1, 2 * H * K + HV * V + 256)), "differ in width"),
+    (lambda r: r["production_out"].__setitem__(1, torch.zeros(1, HV * V - 1)), "production_out"),
 ])
 def test_malformed_records_are_refused(tmp_path, break_it, needle):
     rec = _record()
