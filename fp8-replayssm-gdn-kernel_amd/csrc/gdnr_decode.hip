@@ -372,7 +372,8 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
     u32x4_t packed[2];
 #pragma unroll
     for (int ii = 0; ii < 2; ++ii) {
-      // P on the ring tokens, and on the query as a block of its own (row 0)
+      // P on the ring tokens, and on the query as a block of its own (every
+      // A row is q; output row 0 is the one used)
       f32x4_t pr = {0.f, 0.f, 0.f, 0.f}, pq = pr;
       int xo = kLX + l16 * kXStride + 64 * q4, qo = kLQK + 64 * q4;
       asm volatile("" : "+v"(xo), "+v"(qo));  // read in the loop, not held across it
@@ -382,7 +383,7 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
         const u32x4_t qx = *(const u32x4_t*)(uu + qo + 16 * m);
         const u32x4_t bv = codes8(c[ii], m);
         pr = mfma16(x, bv, pr);
-        pq = mfma16(l16 == 0 ? qx : u32x4_t{0u, 0u, 0u, 0u}, bv, pq);
+        pq = mfma16(qx, bv, pq);
       }
       float wv[4], post[4], dqt[4];
 #pragma unroll
@@ -403,7 +404,8 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
       for (int e = 0; e < 4; ++e) uv = __builtin_amdgcn_mfma_f32_16x16x4f32(rrv[e], wv[e], uv, 0, 0, 0);
       // o = S_n q = lam (S_0 q) + sum_t U~_t (k_t . q): this lane's share
       float ut[4];
-      float o = (lamv * scp) * pq[0];  // (zero at lanes q4 != 0)
+      // (pq[0] is S_0 q at every q4: counted at q4 == 0 only)
+      float o = (q4 == 0 ? lamv * scp : 0.f) * pq[0];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         ut[e] = uv[e] * post[e];
