@@ -425,18 +425,28 @@ def main() -> int:
 # cycle, split against fused), BASELINE configs 1 and 3, and the HBM floor.
 # ---------------------------------------------------------------------------
 
+GRAPH_MIN_LAUNCHES = 192
+
+
 def _graph_us(stream, one_round, calls: int, rounds: int = 3, warm: int = 1) -> float:
     """Microseconds per launch: one_round() (`calls` launches) run once
-    eagerly, captured in a HIP graph, replayed `warm` + `rounds` times, HIP
-    events on the capture stream around the timed replays."""
+    eagerly, then captured in a HIP graph as many times in a row as makes
+    at least GRAPH_MIN_LAUNCHES launches, replayed `warm` + `rounds` times,
+    HIP events on the capture stream around the timed replays. (Each replay
+    of a graph costs microseconds between its last launch and the next
+    replay's first, which a graph of a dozen launches would spread over
+    them: the kernel trace then shows the launches shorter than the events
+    say.)"""
     import torch
 
+    reps = max(1, math.ceil(GRAPH_MIN_LAUNCHES / calls))
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.stream(stream):
         one_round()
         stream.synchronize()
         with torch.cuda.graph(graph, stream=stream):
-            one_round()
+            for _ in range(reps):
+                one_round()
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     with torch.cuda.stream(stream):
@@ -447,7 +457,7 @@ def _graph_us(stream, one_round, calls: int, rounds: int = 3, warm: int = 1) -> 
             graph.replay()
         end.record(stream)
     torch.cuda.synchronize()
-    return start.elapsed_time(end) * 1e3 / (rounds * calls)
+    return start.elapsed_time(end) * 1e3 / (rounds * reps * calls)
 
 
 def _core_sets(B: int, L: int, S: int, device, seed: int) -> list:

@@ -929,10 +929,14 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
   // vblock sooner)
   uint8_t* ck_rows = sbase(ckpt, bs, ck_b) + (hv * ck_h + R0 * ck_v);
   u32x4_t cw[TPW][2];
+  // (non-temporal: the codes are read once per step and not again before the
+  // next step's, which a decode batch of any size finds evicted; the hint
+  // keeps them from displacing the rings and the step's other data in L2
+  // and the Infinity Cache. Measured 11.44 vs 11.96 us/step at B=64, L=16.)
   auto load_tile = [&](int i) {
     const uint32_t off = (uint32_t)(32 * (i >> 1) + 2 * l16 + (i & 1)) * ck_v + 32 * q4;
-    cw[i][0] = *(g_u32x4*)(ck_rows + off);
-    cw[i][1] = *(g_u32x4*)(ck_rows + off + 16);
+    cw[i][0] = __builtin_nontemporal_load((g_u32x4*)(ck_rows + off));
+    cw[i][1] = __builtin_nontemporal_load((g_u32x4*)(ck_rows + off + 16));
   };
   load_tile(0);
   load_tile(1);

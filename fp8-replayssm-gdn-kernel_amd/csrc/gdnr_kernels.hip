@@ -234,12 +234,16 @@ __global__ __launch_bounds__(256) void replay_kernel(const ReplayArgs a) {
     dtb_bits = ((const uint32_t*)a.dt_bias)[(int64_t)hv * a.db_s];
   }
 
-  // ---- 3. checkpoint tile -> VGPRs ---------------------------------------
+  // ---- 3. checkpoint tile -> VGPRs (non-temporal: read once per step) ------
   GDNR_COMPILER_FENCE();
   uint4 ck[NCH];
   uint8_t* ckp = a.ckpt + (int64_t)b * a.ck_b + (int64_t)hv * a.ck_h + (int64_t)(v0 + gm) * a.ck_v + 16 * gi;
 #pragma unroll
-  for (int j = 0; j < NCH; ++j) ck[j] = *(const uint4*)(ckp + (int64_t)(8 * j) * a.ck_v);
+  for (int j = 0; j < NCH; ++j) {
+    typedef uint32_t u32x4_nt __attribute__((ext_vector_type(4)));
+    const u32x4_nt v = __builtin_nontemporal_load((const u32x4_nt*)(ckp + (int64_t)(8 * j) * a.ck_v));
+    ck[j] = make_uint4(v[0], v[1], v[2], v[3]);
+  }
   GDNR_COMPILER_FENCE();
   // ---- 4. all but the checkpoint tile has landed --------------------------
   GDNR_WAIT_VMCNT(NCH);
