@@ -144,12 +144,21 @@ def test_replay_block_v_and_split_identical(device):
 
 
 def test_replay_full_size_config1(device):
-    """Config 1 shape: B=64, Qwen3.5-4B layer, L=16, fills uniform in 1..16."""
-    case = make_replay_case(64, 16, device, seed=0, warmup=256)
+    """Config 1 as defined: B=64, Qwen3.5-4B layer, L=16, fills uniform in
+    1..16, the sequences at fill 16 flushing in the same launch (rebuild,
+    emit from the rebuilt state, requantise in place)."""
+    gen = torch.Generator(device="cpu").manual_seed(1)
+    valid = torch.randint(1, 17, (64,), generator=gen, dtype=torch.int32)
+    valid[:4] = 16  # at least four flushing sequences
+    case = make_replay_case(64, 16, device, seed=0, warmup=256, valid=valid, flush=valid == 16)
     out = run_replay(case, block_v=128)
-    ref, _, _ = oracle_replay(case, np.float32)
+    ref, ref_codes, ref_scale = oracle_replay(case, np.float32)
     err = rel_l2(np32(out), ref)
     assert err <= OUT_TOL, err
+    fl = (valid == 16).numpy()
+    codes = codes_np(case["ckpt"].payload)
+    assert np.mean(codes[fl] != ref_codes[fl]) < 1e-3
+    assert np.array_equal(codes[~fl], case["codes0"][~fl])  # replays leave their checkpoints alone
 
 
 @pytest.mark.parametrize("ring_len,block_v", [(4, 32), (16, 128), (64, 64)])
