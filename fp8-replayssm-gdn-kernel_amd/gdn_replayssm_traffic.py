@@ -183,14 +183,62 @@ def reduce_pmc(fetch_dir, write_dir, kernel: str, calib_bytes: int, calib_copies
     return result
 
 
+def trace_by_fill(run_dir, kernel: str, sets: int, window: int, rounds: int = 2) -> dict:
+    """Launch durations of ``kernel`` by ring fill from a rocprofv3
+    --kernel-trace run of ``bench.py --profile``: the last ``rounds`` rounds
+    of sets x window launches, launch i at fill (i // sets) % window + 1 (the
+    bench's cycle). Returns {fill: (mean, min, max) us}, the cycle mean, and
+    the median gap between consecutive launches."""
+    import csv
+    import statistics
+    from pathlib import Path
+
+    files = sorted(Path(run_dir).rglob("*kernel_trace.csv"))
+    if not files:
+        raise FileNotFoundError(f"no *kernel_trace.csv under {run_dir}")
+    rows = []
+    for f in files:
+        with open(f, newline="") as fh:
+            rows += [r for r in csv.DictReader(fh) if kernel in r["Kernel_Name"]]
+    rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+    last = rows[-rounds * sets * window:]
+    if len(last) < rounds * sets * window:
+        raise ValueError(f"{len(rows)} launches of {kernel!r}, fewer than {rounds} rounds")
+    by = {f: [] for f in range(1, window + 1)}
+    for i, r in enumerate(last):
+        by[(i // sets) % window + 1].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    table = {f: (statistics.mean(v), min(v), max(v)) for f, v in by.items()}
+    gaps = [(int(b["Start_Timestamp"]) - int(a["End_Timestamp"])) / 1e3 for a, b in zip(last, last[1:])]
+    return {"by_fill": table, "cycle_mean_us": statistics.mean(m for m, _, _ in table.values()),
+            "gap_median_us": statistics.median(gaps), "kernel": rows[-1]["Kernel_Name"]}
+
+
 if __name__ == "__main__":
     import argparse
     import json
+    import sys
+
+    if "--trace" in sys.argv:
+        p = argparse.ArgumentParser(description="Launch durations by ring fill from a rocprofv3 kernel trace")
+        p.add_argument("--trace", required=True, help="rocprofv3 -d directory of the --kernel-trace run")
+        p.add_argument("--kernel", default="decode_kernel", help="substring of the kernel name")
+        p.add_argument("--sets", type=int, default=12)
+        p.add_argument("--window", type=int, default=16)
+        args = p.parse_args()
+        res = trace_by_fill(args.trace, args.kernel, args.sets, args.window)
+        print(f"kernel: {res['kernel']}")
+        print("| fill | " + " | ".join(str(f) for f in res["by_fill"]) + " |")
+        print("|---" * (len(res["by_fill"]) + 1) + "|")
+        for k, name in enumerate(("mean us", "min us", "max us")):
+            print(f"| {name} | " + " | ".join(f"{v[k]:.2f}" for v in res["by_fill"].values()) + " |")
+        print(f"cycle mean {res['cycle_mean_us']:.2f} us per launch; median gap between launches "
+              f"{res['gap_median_us']:.2f} us")
+        sys.exit(0)
 
     p = argparse.ArgumentParser(description="Reduce rocprofv3 FETCH_SIZE / WRITE_SIZE runs to HBM bytes per launch")
     p.add_argument("--fetch", required=True, help="rocprofv3 -d directory of the FETCH_SIZE run")
     p.add_argument("--write", required=True, help="rocprofv3 -d directory of the WRITE_SIZE run")
-    p.add_argument("--kernel", default="step_kernel", help="substring of the kernel name")
+    p.add_argument("--kernel", default="decode_kernel", help="substring of the kernel name")
     p.add_argument("--calib-bytes", type=int, default=64 << 20)
     p.add_argument("--calib-copies", type=int, default=4)
     p.add_argument("--algorithmic-bytes", type=float, default=None,
