@@ -625,12 +625,13 @@ def config3(device, stream, windows=(4, 16, 64), B: int = 8, steps: int = 4096,
                      g=torch.zeros(B, L, HV, **bf), beta=torch.zeros(B, L, HV, **bf),
                      out=torch.empty(B, HV, V, **bf)) for _ in range(S)]
         fills = [torch.full((B,), f, dtype=torch.int32, device=device) for f in range(1, L + 1)]
+        poss = [f - 1 for f in fills]  # (formed here: inside the timed cycle they would be a kernel per step)
         flushes = [torch.full((B,), f == L, dtype=torch.bool, device=device) for f in range(1, L + 1)]
 
         def cycle():
             for i in range(S * L):
                 st, c = sets[i % S], (i // S) % L
-                gk.gdn_prep_replay_fp8(mixed[c], a_raw[c], b_raw[c], a_log, dt_bias, fills[c] - 1, st["payload"],
+                gk.gdn_prep_replay_fp8(mixed[c], a_raw[c], b_raw[c], a_log, dt_bias, poss[c], st["payload"],
                                        st["scale"], st["q_out"], st["k"], st["v"], st["g"], st["beta"], fills[c],
                                        flushes[c], block_v=128, out=st["out"])
 
