@@ -15,7 +15,8 @@
 // The order of steps 2-3 is pinned with compiler fences.
 // These kernels serve rings longer than 16 tokens, the split path, the
 // standalone prep and the quantiser; rings of up to 16 tokens go through the
-// step kernel (gdnr_step.hip).
+// decode kernel (gdnr_decode.hip, 16-bit activations) or the step kernel
+// (gdnr_step.hip, f32 activations).
 //
 // This file is compiled once per activation dtype: GDNR_ACT=0 (bf16, also
 // holds the dtype-free quantiser kernels), 1 (f16), 2 (f32).

@@ -115,3 +115,23 @@ def test_long_ring_fused_equals_prep_then_replay(device):
         results.append([out, q_out, rk, rv, rg, rb, ck.payload.view(torch.uint8), ck.scale])
     for x, y in zip(*results):
         assert torch.equal(x, y)
+
+
+def test_long_ring_tiles_identical(device):
+    """The V-tile height of the long-ring kernel (block_v 32, 64 or 128; the
+    library also lowers it on its own for small launches) changes nothing:
+    outputs, requantised codes and scales are bit-identical at L = 64, with
+    replaying and flushing sequences in the same launch. (Batch 16: no tile
+    is lowered below the requested one.)"""
+    from gpu_helpers import make_replay_case, run_replay
+
+    valid = [64, 17, 33, 64, 1, 64, 50, 63, 64, 2, 40, 64, 9, 64, 31, 64]
+    flush = [v == 64 for v in valid]
+    results = []
+    for bv in (128, 64, 32):
+        case = make_replay_case(16, 64, device, seed=4300, warmup=16, valid=valid, flush=flush)
+        out = run_replay(case, block_v=bv)
+        results.append((out, case["ckpt"].payload.view(torch.uint8).clone(), case["ckpt"].scale.clone()))
+    for other in results[1:]:
+        for x, y in zip(results[0], other):
+            assert torch.equal(x, y)
