@@ -495,7 +495,15 @@ void fit_decode(gdnr::ReplayArgs* a) {
   // and the head groups of a sequence
   const int32_t per_seq = a->H * (a->G / a->gw), waves = 1 + a->gw * a->nwh;
   a->units = 1;
+  // Large launches (at least 16 units per compute unit) keep one unit per
+  // workgroup: four small workgroups share a compute unit, and one's start
+  // (its chain's ring round trip) overlaps the others' streams. At B=512,
+  // L=8: 80.1 us per step against 86.3 with 4-unit workgroups (one per
+  // compute unit, run one after another); at B=128 4 units win, 21.5 us
+  // against 22.8.
+  const bool large = (int64_t)a->B * per_seq >= 16 * (int64_t)cus;
   for (int32_t u : {4, 2}) {
+    if (large) break;
     const int32_t hp = u == 4 ? 2 : 1, sp = u / hp;
     if (a->B % sp == 0 && per_seq % hp == 0 && u * waves <= 12 && (int64_t)a->B * per_seq / u >= cus) {
       a->units = u;

@@ -434,37 +434,25 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
       }
     }
     // pass 1: S_n of the vblock's 2 x 8 column groups (kept) and the vblock
-    // amax (|x| max, NaN propagating like torch.amax)
+    // amax (|x| max, NaN propagating like torch.amax). lam scale S_0 is the
+    // MFMA's accumulator input: lane (nn, q4)'s four outputs of group ct are
+    // the columns of its own code bytes 4 ct .. 4 ct + 3, so each lane forms
+    // them from its codes (one f32 rounding of lam scale x code).
     f32x4_t sv[2][8];
     float am = 0.f;
     {
       const float ls = lamv * scp;
-      uint32_t hbits, lbits;
-      if constexpr (kBF16) {
-        hbits = f32_to_bf16(ls);
-        lbits = f32_to_bf16(ls - __uint_as_float(hbits << 16));
-      } else {
-        const _Float16 hh = (_Float16)ls;
-        hbits = __builtin_bit_cast(uint16_t, hh);
-        lbits = __builtin_bit_cast(uint16_t, (_Float16)(ls - (float)hh));
-      }
-      const uint32_t d0 = l16 == 4 * q4 ? 0xFFFFu : 0u, d1 = l16 == 4 * q4 + 1 ? 0xFFFF0000u : 0u;
-      const uint32_t d2 = l16 == 4 * q4 + 2 ? 0xFFFFu : 0u, d3 = l16 == 4 * q4 + 3 ? 0xFFFF0000u : 0u;
-      const uint32_t h2 = hbits | (hbits << 16), l2 = lbits | (lbits << 16);
-      const u32x4_t a_ls = {h2 & (d0 | d1), h2 & (d2 | d3), l2 & (d0 | d1), l2 & (d2 | d3)};
 #pragma unroll
       for (int ct = 0; ct < 8; ++ct) {
 #pragma unroll
         for (int ii = 0; ii < 2; ++ii) {
-          const uint2 c2 = codes4(c[ii][ct >> 2][ct & 3]);
-          const f32x4_t z = {0.f, 0.f, 0.f, 0.f};
-          const f32x4_t s0 = mfma16(a_ls, u32x4_t{c2.x, c2.y, c2.x, c2.y}, z);
+          const uint32_t cw4 = c[ii][ct >> 2][ct & 3];
+          const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)cw4, false);
+          const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)cw4, true);
+          const f32x4_t s0 = {ls * lo[0], ls * lo[1], ls * hi[0], ls * hi[1]};
           const uint2 k2 = *(const uint2*)(uu + kLKT + 2 * ((ct * 16 + l16) * 16 + 4 * q4));
           sv[ii][ct] = mfma16(u32x4_t{k2.x, k2.y, k2.x, k2.y}, packed[ii], s0);
         }
-        // (a group's first product completes into its second before the
-        // next group starts: no more than one intermediate is held)
-        __builtin_amdgcn_sched_barrier(0);
       }
 #pragma unroll
       for (int ct = 0; ct < 8; ++ct) {
