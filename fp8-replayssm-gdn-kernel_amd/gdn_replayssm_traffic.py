@@ -183,6 +183,40 @@ def reduce_pmc(fetch_dir, write_dir, kernel: str, calib_bytes: int, calib_copies
     return result
 
 
+RDREQ_COUNTERS = ("TCC_EA0_RDREQ_sum", "TCC_EA0_RDREQ_32B_sum", "TCC_EA0_RDREQ_64B_sum", "TCC_EA0_RDREQ_128B_sum")
+
+
+def reduce_rdreq(run_dir, kernel: str, calib_bytes: int, calib_copies: int) -> dict:
+    """Read bytes per launch of ``kernel`` from the L2-to-memory read request
+    counts of one rocprofv3 --pmc run (RDREQ_COUNTERS): 32 n_32B + 64 n_64B +
+    128 n_128B bytes per dispatch, with no calibration factor. The last
+    ``calib_copies`` dispatches are plain copies of ``calib_bytes``; their
+    figure shows whether the three sizes account for every request and byte
+    (a cross-check of the FETCH_SIZE calibration)."""
+    rows = _counter_rows(run_dir)
+    per = {}
+    names = {}
+    for dispatch, name, cname, value in rows:
+        if cname in RDREQ_COUNTERS:
+            per.setdefault(dispatch, {})[cname] = per.get(dispatch, {}).get(cname, 0.0) + value
+            names[dispatch] = name
+    order = sorted(per)
+
+    def stats(ds):
+        tot = {c: sum(per[d].get(c, 0.0) for d in ds) / len(ds) for c in RDREQ_COUNTERS}
+        n_all, n32, n64, n128 = (tot[c] for c in RDREQ_COUNTERS)
+        return {"requests": n_all, "req_32B": n32, "req_64B": n64, "req_128B": n128,
+                "unsized_requests": n_all - n32 - n64 - n128, "bytes": 32 * n32 + 64 * n64 + 128 * n128}
+
+    calib = stats(order[-calib_copies:])
+    launches = [d for d in order if kernel in names[d]]
+    if not launches:
+        raise ValueError(f"no dispatch of {kernel!r} in {run_dir}")
+    res = stats(launches)
+    return {"kernel": kernel, "dispatches": len(launches), **res,
+            "copy": {**calib, "expected_bytes": calib_bytes, "bytes_over_expected": calib["bytes"] / calib_bytes}}
+
+
 def trace_by_fill(run_dir, kernel: str, sets: int, window: int, rounds: int = 2) -> dict:
     """Launch durations of ``kernel`` by ring fill from a rocprofv3
     --kernel-trace run of ``bench.py --profile``: the last ``rounds`` rounds
@@ -218,6 +252,21 @@ if __name__ == "__main__":
     import json
     import sys
 
+    if "--rdreq" in sys.argv:
+        p = argparse.ArgumentParser(description="Read bytes per launch from L2-to-memory request counts")
+        p.add_argument("--rdreq", required=True, help="rocprofv3 -d directory of the RDREQ_COUNTERS run")
+        p.add_argument("--kernel", default="decode_kernel", help="substring of the kernel name")
+        p.add_argument("--calib-bytes", type=int, default=64 << 20)
+        p.add_argument("--calib-copies", type=int, default=4)
+        p.add_argument("--out", default=None)
+        args = p.parse_args()
+        res = reduce_rdreq(args.rdreq, args.kernel, args.calib_bytes, args.calib_copies)
+        if args.out:
+            with open(args.out, "w") as fh:
+                json.dump(res, fh, indent=1)
+                fh.write("\n")
+        print(json.dumps(res, indent=1))
+        sys.exit(0)
     if "--trace" in sys.argv:
         p = argparse.ArgumentParser(description="Launch durations by ring fill from a rocprofv3 kernel trace")
         p.add_argument("--trace", required=True, help="rocprofv3 -d directory of the --kernel-trace run")
