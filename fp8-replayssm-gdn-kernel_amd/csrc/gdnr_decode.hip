@@ -27,14 +27,15 @@
 // coefficient chain (or flush factors) and publishes them through LDS; the
 // others wait for its flag only after their own projections are done.
 //
-// Operand layouts (16x16x32 MFMA; lane = 16 q4 + l16):
-//   X (A operand): lane (t = l16, q4) holds X[t][kappa(m, q4) + 0..7] for
-//     k-step m = 0..3, kappa(m, q4) = 64 (m >> 1) + 16 q4 + 8 (m & 1): the
-//     32 bytes at 32 q4 and at 128 + 32 q4 of the row.
+// Operand layouts (16x16x32 MFMA; lane = 16 q4 + l16; k-step m = 0..3 of a
+// lane covers columns 32 q4 + 8 m + 0..7):
+//   X (A operand): lane (t = l16, q4) holds X[t][32 q4 + 8 m + 0..7]: the
+//     64 bytes at 64 q4 of the row (elements 32 q4 .. 32 q4 + 31).
 //   codes (B operand) of tile i (16 rows): lane (nn = l16, q4) holds row
 //     r(i, nn) = 32 (i >> 1) + 2 nn + (i & 1) of the wave's rows, bytes
-//     [16 q4, +16) and [64 + 16 q4, +16). Tiles 2p, 2p + 1 are vblock p of
-//     the wave, and a lane's rows of a token's v sit in two 4-byte pairs.
+//     [32 q4, +32) (the codes of the same columns). Tiles 2p, 2p + 1 are
+//     vblock p of the wave, and a lane's rows of a token's v sit in two
+//     4-byte pairs.
 //   P (accumulator): lane (nn, q4) holds P[token 4 q4 + e][row r(i, nn)].
 //
 // Compiled once per 16-bit activation dtype (GDNR_ACT = 0 bf16, 1 f16).
@@ -83,7 +84,8 @@ __device__ __forceinline__ f32x4_t mfma16(u32x4_t a, u32x4_t b, f32x4_t c) {
 }
 // 4 e4m3 codes -> 4 values of the activation type (exact), packed in pairs
 __device__ __forceinline__ uint2 codes4(uint32_t w) { return kBF16 ? fp8x4_to_bf16x4(w) : fp8x4_to_f16x4(w); }
-// the 8 codes of k-step m of a row's 32 bytes (c[0]: bytes at 16 q4, c[1]: at 64 + 16 q4)
+// the 8 codes of k-step m of a lane's 32 bytes of a row (c[0]: bytes
+// [32 q4, +16), c[1]: [32 q4 + 16, +16); k-step m: bytes 32 q4 + 8 m + 0..7)
 __device__ __forceinline__ u32x4_t codes8(const u32x4_t* c, int m) {
   const u32x4_t w = c[m >> 1];
   const uint32_t w0 = (m & 1) ? w[2] : w[0], w1 = (m & 1) ? w[3] : w[1];
@@ -707,8 +709,9 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
     const float dq = on ? (full ? Dq[l16] : Gs[l16 * 16 + (full ? 0 : n)]) : 0.f;
     if (do_flush) {
       // K^T operand tiles [ct][M][token] (flush): element (t, col) of X with
-      // col = kappa(m, q4) + j8 goes to tile ct = 2 m + j8 / 4, row
-      // M = 4 q4 + j8 % 4; tokens t >= n are zero
+      // col = 32 q4 + 8 m + j8 goes to tile ct = 2 m + j8 / 4, row
+      // M = 4 q4 + j8 % 4 (tile ct, row M: column 32 (M >> 2) + 4 ct + (M & 3));
+      // tokens t >= n are zero
       uint16_t* kt = (uint16_t*)(ul + kLKT);
 #pragma unroll
       for (int m = 0; m < 4; ++m) {
