@@ -516,6 +516,7 @@ void fit_decode(gdnr::ReplayArgs* a) {
 int launch_decode(const gdnr::ReplayArgs& r, int act, bool fused, bool gate_f32, void* stream) {
   gdnr::StepArgs a = make_step_args(r, elem_size(act), gate_f32 ? 4 : elem_size(act));
   a.status = gdnr::status_word();
+  a.wait_polls = gdnr::wait_polls();
   if (act == GDNR_DTYPE_BF16) return gdnr::launch_decode_bf16(a, fused, gate_f32, stream);
   return gdnr::launch_decode_f16(a, fused, gate_f32, stream);
 }
@@ -528,6 +529,7 @@ int launch_replay(const gdnr::ReplayArgs& a, int act, int mode, bool gate_f32, v
 int launch_step(const gdnr::ReplayArgs& r, int act, bool fused, bool gate_f32, void* stream) {
   gdnr::StepArgs a = make_step_args(r, elem_size(act), gate_f32 ? 4 : elem_size(act));
   a.status = gdnr::status_word();
+  a.wait_polls = gdnr::wait_polls();
   if (act == GDNR_DTYPE_BF16) return gdnr::launch_step_bf16(a, fused, gate_f32, stream);
   if (act == GDNR_DTYPE_F16) return gdnr::launch_step_f16(a, fused, gate_f32, stream);
   return gdnr::launch_step_f32(a, fused, gate_f32, stream);
@@ -554,9 +556,14 @@ int check_prep_inputs(const gdnr_tensor* mixed_qkv, const gdnr_tensor* a, const 
   if (mixed_qkv->dtype != g.act)
     return fail(GDNR_ERR_INVALID_ARGUMENT, "mixed_qkv: dtype %s differs from the ring dtype %s",
                 dtype_name(mixed_qkv->dtype), dtype_name(g.act));
+  // rows of at least 2 H K + HV V elements: the preparation reads the first
+  // 2 H K + HV V of each row (q heads | k heads | v heads, kernel:500-550) and
+  // steps between rows by the row stride, so a wider row buffer is accepted
+  // as the reference accepts it
   const int64_t width = 2 * g.H * g.K + g.HV * g.V;
-  if (mixed_qkv->shape[0] != g.B || mixed_qkv->shape[1] != width)
-    return fail(GDNR_ERR_INVALID_ARGUMENT, "mixed_qkv: shape [%lld, %lld], expected [%lld, %lld] (2 H K + HV V)",
+  if (mixed_qkv->shape[0] != g.B || mixed_qkv->shape[1] < width)
+    return fail(GDNR_ERR_INVALID_ARGUMENT,
+                "mixed_qkv: shape [%lld, %lld], expected [%lld, >= %lld] (2 H K + HV V)",
                 (long long)mixed_qkv->shape[0], (long long)mixed_qkv->shape[1], (long long)g.B, (long long)width);
   GDNR_TRY(check_inner_unit(mixed_qkv, "mixed_qkv"));
   GDNR_TRY(check_align(mixed_qkv, "mixed_qkv", 2 * elem_size(g.act)));
@@ -654,6 +661,28 @@ int gdnr_wait_timeouts(uint32_t* count, int32_t reset) {
   if (!count) return fail(GDNR_ERR_INVALID_ARGUMENT, "count is NULL");
   const int rc = gdnr::read_status(count, reset != 0);
   if (rc) return fail(GDNR_ERR_HIP, "reading the wait status word failed: %s", gdnr::hip_error_string(rc));
+  return GDNR_OK;
+}
+
+uint32_t gdnr_set_wait_polls(uint32_t polls) { return gdnr::set_wait_polls(polls); }
+
+int gdnr_decode_plan(int32_t batch, int32_t heads, int32_t value_heads, int32_t value_dim, int32_t ring_len,
+                     int32_t act_dtype, int32_t* plan) {
+  g_last_error.clear();
+  if (!plan) return fail(GDNR_ERR_INVALID_ARGUMENT, "plan is NULL");
+  if (batch <= 0 || heads <= 0 || value_heads <= 0 || value_heads % heads != 0 || ring_len <= 0)
+    return fail(GDNR_ERR_INVALID_ARGUMENT, "batch, heads, value_heads (a multiple of heads) and ring_len must be > 0");
+  gdnr::ReplayArgs a = {};
+  a.B = batch, a.H = heads, a.HV = value_heads, a.G = value_heads / heads, a.V = value_dim, a.L = ring_len;
+  if (!decode_eligible(a, act_dtype))
+    return fail(GDNR_ERR_UNSUPPORTED, "no decode-kernel plan: 16-bit activations, L <= %d, V in {64, 128, 256}",
+                gdnr::kStepRing);
+  fit_decode(&a);
+  plan[0] = a.V / a.nwh;
+  plan[1] = a.nwh;
+  plan[2] = a.gw;
+  plan[3] = a.units;
+  plan[4] = a.lds_bytes;
   return GDNR_OK;
 }
 

@@ -238,9 +238,11 @@ constexpr int kHLam = kHCoef + 64;             // f32 [4]: lam, the scale of the
 constexpr int kHFac = kHLam + 16;              // float4 [16]: (pre, post, dq, 0) (flush)
 constexpr int kHT0 = kHFac + 256;              // act [3][128]: T_0 as hi, mid and lo rows (replay)
 constexpr int kHM = kHT0;                      // f32 [16][16]: M (chain scratch; flush, so T_0's bytes;
-                                               // then the helpers' o partials, [2][64] float2)
+                                               // then the helpers' o partials, [kPartials][64] float2)
 constexpr int kHR = kHM + 1024;                // f32 [16][16]: R = (I + M)^-1 (flush)
 constexpr int kHeadLds = kHR + 1024;
+constexpr int kPartials = 2;                   // helper o partials per value head (512 bytes each, in M's area)
+static_assert(kPartials * 512 <= kHR - kHM, "the helpers' o partials must fit M's area");
 constexpr int kMaxDecodeHeads = 2;            // value heads per unit (gw)
 constexpr int kUnitBase = kLHeads + kMaxDecodeHeads * kHeadLds;  // LDS of one unit before its v rows
 // then per row wave: its v rows, token-major ([16][64 vb + 16] bytes), and
@@ -251,12 +253,14 @@ __host__ __device__ constexpr int row_wave_lds(int vb) { return kStepRing * (64 
 // Vblocks of each row wave of a flushing unit that helpers rebuild (the
 // last ones), given nhelp helper waves: the smallest longest chain
 // max(vb - k, ceil(rpu k / nhelp)), at most one per helper (each helper job
-// needs a buffer: the helped row wave's, or the partner unit's second).
-// nhelp is 0 when the partner unit flushes too: the workgroup's SIMDs are
-// then busy with row waves, and a helper only lengthens the launch.
-__device__ __forceinline__ int helper_vblocks(int vb, int rpu, int nhelp) {
+// needs a buffer: the helped row wave's, or the partner unit's second), and
+// at most kPartials / nwh per row wave (a value head's nwh row waves share
+// its kPartials o-partial slots). nhelp is 0 when the partner unit flushes
+// too: the workgroup's SIMDs are then busy with row waves, and a helper only
+// lengthens the launch.
+__device__ __forceinline__ int helper_vblocks(int vb, int rpu, int nhelp, int nwh) {
   int best = vb, kb = 0;
-  for (int k = 1; k < vb && k <= nhelp; ++k) {
+  for (int k = 1; k < vb && k <= nhelp && k * nwh <= kPartials; ++k) {
     const int crit = max(vb - k, (rpu * k + nhelp - 1) / nhelp);
     if (crit < best) {
       best = crit;
@@ -359,7 +363,9 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
   // rebuilds the last ones of a flushing unit's row waves (the helpers
   // below). uu: the unit's LDS block, hb: the head's, vr: the row wave's v
   // rows, nf: the ring fill, c: the vblock's codes (cur layout), scp: its
-  // scale, rows: the row wave's checkpoint rows. Returns the new scale and
+  // scale, rows: the row wave's checkpoint rows, st: false when a wait the
+  // rebuild depends on gave up (the codes are then not stored, the checkpoint
+  // stays as it was). Returns the new scale and
   // this lane's shares op[ii] of o for the two tiles; after_pass1() runs once
   // the codes are no longer needed.
   //
@@ -369,7 +375,7 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
   // into hi + lo halves; each hi/lo pair is one 16x16x32 MFMA (k-slots
   // 8 q4 + j: j < 4 the hi part, j >= 4 the lo part of column 4 q4 + (j & 3)).
   auto flush_vblock = [&](const uint8_t* uu, const uint8_t* hb, const uint8_t* vr, int nf, const u32x4_t (&c)[2][2],
-                          float scp, uint8_t* rows, int p, float* op, auto&& after_pass1) -> float {
+                          float scp, uint8_t* rows, int p, bool st, float* op, auto&& after_pass1) -> float {
     const float lamv = ((const float*)(hb + kHLam))[0];
     u32x4_t packed[2];
 #pragma unroll
@@ -486,7 +492,7 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
           uint32_t wd[4];
 #pragma unroll
           for (int w4 = 0; w4 < 4; ++w4) wd[w4] = quant(sv[ii][4 * hh + w4]);
-          *(g_u32x4_w*)(rows + ro + 16 * hh) = u32x4_t{wd[0], wd[1], wd[2], wd[3]};
+          if (st) *(g_u32x4_w*)(rows + ro + 16 * hh) = u32x4_t{wd[0], wd[1], wd[2], wd[3]};
         }
       }
     };
@@ -622,7 +628,7 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
       }
       hv_unit = uni(hv_unit);
       if (hv_unit >= 0 && nhelp > 0) {
-        h_nh = uni(helper_vblocks(VB, rpu, nhelp));
+        h_nh = uni(helper_vblocks(VB, rpu, nhelp, NWH));
         const int jobs = h_nh * rpu, per = (jobs + nhelp - 1) / nhelp;
         h_g0 = uni(hidx * per);
         h_g1 = uni(min(jobs, h_g0 + per));
@@ -867,7 +873,9 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
 
       uint8_t* const uv = lds + hv_unit * unit_lds(rpu, VB);
       int* const vflags = (int*)(uv + kLFlag);
-      if (hv_unit != u) wait_flag(vflags + kFlagReady, a.status);
+      // (a wait that gives up leaves the checkpoint alone: the job's codes
+      // and scale are not stored, its flags still raised)
+      bool h_ok = hv_unit == u || wait_flag(vflags + kFlagReady, a.status, a.wait_polls);
       uint32_t nsc = 0;
       uint8_t* sc_addr = nullptr;
 #pragma unroll
@@ -877,7 +885,7 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
         const int kk = g / rpu, wv = g % rpu, pv = VB - h_nh + kk;
         if (h_g1 - h_g0 == 2) GDNR_WAIT_VMCNT(4);
         else GDNR_WAIT_VMCNT(0);
-        wait_flag(vflags + kFlagVStaged + wv, a.status);
+        h_ok = wait_flag(vflags + kFlagVStaged + wv, a.status, a.wait_polls) && h_ok;
         const uint8_t* buf = job_buf(kk, wv);
         u32x4_t c[2][2];
 #pragma unroll
@@ -889,7 +897,8 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
         const uint8_t* hbv = uv + kLHeads + (wv / NWH) * kHeadLds;
         float op[2];
         const float s32 =
-            flush_vblock(uv, hbv, uv + kUnitBase + wv * row_wave_lds(VB), h_nf, c, scp, job_rows(wv), pv, op, []() {});
+            flush_vblock(uv, hbv, uv + kUnitBase + wv * row_wave_lds(VB), h_nf, c, scp, job_rows(wv), pv, h_ok, op,
+                         []() {});
         *(float2*)(hbv + kHM + 512 * (partj * h_nh + kk) + 8 * lane) = make_float2(op[0], op[1]);
         GDNR_WAIT_LGKM0();
         if (lane == 0)
@@ -897,7 +906,10 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
         nsc = lane == jj ? (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)s32) : nsc;
         sc_addr = lane == jj ? sc_j : sc_addr;
       }
-      if (lane < h_g1 - h_g0) *(uint16_t*)sc_addr = (uint16_t)nsc;
+      if (h_ok && lane < h_g1 - h_g0) *(uint16_t*)sc_addr = (uint16_t)nsc;
+      // (a job whose wait gave up stored nothing, so the count-based waits
+      // above may have under-counted its DMA: drain it before the wave ends)
+      if (!h_ok) GDNR_WAIT_VMCNT(0);
     }
     return;
   }
@@ -945,7 +957,7 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
     for (int i = 2; i < TPW; ++i) load_tile(i);
   } else {
     const int nhelp = has_partner ? (partner_flushes(A) ? 0 : 2) : 1;
-    nh = uni(helper_vblocks(VB, rpu, nhelp));
+    nh = uni(helper_vblocks(VB, rpu, nhelp, NWH));
   }
   uint8_t* scale_hv = sbase(A.scale, bs, A.sc_b) + (hv * A.sc_h);
   const int vb0 = R0 / kVBlock;
@@ -977,7 +989,9 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
   // the chain wave's LDS blocks are complete once its flag is set (a flag,
   // not a workgroup barrier: the waves of a flushing unit need not wait for
   // the other units' row waves to get their loads issued)
-  wait_flag((int*)(ul + kLFlag) + kFlagReady, A.status);
+  // (a wait that gives up: the step's output is meaningless, and a flush
+  // stores no codes or scales)
+  const bool ready_ok = wait_flag((int*)(ul + kLFlag) + kFlagReady, A.status, A.wait_polls);
 
   // ring append of the new token's v rows (full contract; this wave's rows,
   // which no other wave reads): the lanes that loaded token pos. (The flush
@@ -1082,7 +1096,7 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
 #pragma unroll
     for (int q = 1; q < VB; ++q) scp = p == q ? sct[q] : scp;
     float op[2];
-    const float s32 = flush_vblock(ul, hl, vl, n, cur, scp, ck_rows, p, op, [&]() {
+    const float s32 = flush_vblock(ul, hl, vl, n, cur, scp, ck_rows, p, ready_ok, op, [&]() {
       // the next vblock's codes from the prefetch buffer (into the same
       // registers), then the buffer refilled with the one after
       if (p + 1 < own) {
@@ -1099,7 +1113,7 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
     new_scale = lane == p ? (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)s32) : new_scale;
   }
   if (nh > 0) {
-    wait_count(flags + kFlagHelped + wr, nh, A.status);
+    (void)wait_count(flags + kFlagHelped + wr, nh, A.status, A.wait_polls);  // (the helpers gate their own stores)
     for (int kk = 0; kk < nh; ++kk) {
       const int p = own + kk;
       const float2 o2 = *(const float2*)(hl + kHM + 512 * (part * nh + kk) + 8 * lane);
@@ -1110,7 +1124,10 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
 #pragma unroll
   for (int g = 0; g < TPW / 4; ++g)
     store_out(g, opart_all[4 * g], opart_all[4 * g + 1], opart_all[4 * g + 2], opart_all[4 * g + 3]);
-  if (lane < own) *(uint16_t*)(scale_hv + (vb0 + lane) * A.sc_v) = (uint16_t)new_scale;
+  if (ready_ok && lane < own) *(uint16_t*)(scale_hv + (vb0 + lane) * A.sc_v) = (uint16_t)new_scale;
+  // (with no code stores the loop's count-based DMA waits may have
+  // under-counted: drain the last prefetch before the wave ends)
+  if (!ready_ok) GDNR_WAIT_VMCNT(0);
   if constexpr (FUSED) {
     if (pos >= 0 && lane < CPT) {
       uint8_t* vw = sbase(A.v, bs, A.v_b) + ((uint32_t)pos * A.v_t + hv * A.v_h + R0 * ES) + 16 * lane;

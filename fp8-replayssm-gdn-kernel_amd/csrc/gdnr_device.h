@@ -275,10 +275,12 @@ __device__ __forceinline__ int wave_sum_i32(int x) {
 __device__ __forceinline__ bool flag_set(int* f) {
   return __builtin_amdgcn_readfirstlane(__hip_atomic_load(f, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP)) != 0;
 }
-// bounded wait for an LDS flag; a wait that gives up is counted in the
-// device status word (gdnr_wait_timeouts) and reported to the caller
-__device__ __forceinline__ bool wait_flag(int* f, uint32_t* status) {
-  for (int it = 0; it < (1 << 22); ++it) {
+// bounded wait for an LDS flag, at most `polls` polls (kWaitPolls unless
+// the host set another budget: gdnr_set_wait_polls); a wait that gives up
+// is counted in the device status word (gdnr_wait_timeouts) and reported to
+// the caller, which then skips its in-place checkpoint stores
+__device__ __forceinline__ bool wait_flag(int* f, uint32_t* status, uint32_t polls) {
+  for (uint32_t it = 0; it < polls; ++it) {
     if (flag_set(f)) return true;
     __builtin_amdgcn_s_sleep(1);
   }
@@ -287,8 +289,8 @@ __device__ __forceinline__ bool wait_flag(int* f, uint32_t* status) {
 }
 
 // bounded wait for an LDS counter to reach `target` (counted like wait_flag)
-__device__ __forceinline__ bool wait_count(int* f, int target, uint32_t* status) {
-  for (int it = 0; it < (1 << 22); ++it) {
+__device__ __forceinline__ bool wait_count(int* f, int target, uint32_t* status, uint32_t polls) {
+  for (uint32_t it = 0; it < polls; ++it) {
     if (__builtin_amdgcn_readfirstlane(__hip_atomic_load(f, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP)) >= target)
       return true;
     __builtin_amdgcn_s_sleep(1);

@@ -69,6 +69,7 @@ struct ReplayArgs {
 
 constexpr int32_t kMaxStepLds = 160 * 1024;  // gfx950 LDS per workgroup
 constexpr int kStepRing = 16;                // ring capacity handled by the step kernel
+constexpr uint32_t kWaitPolls = 1u << 22;     // default poll budget of a bounded LDS wait
 
 // Argument block of the step kernel (gdnr_step.hip), built on the host from a
 // validated ReplayArgs: byte pointers and 32-bit BYTE strides (the host checks
@@ -90,8 +91,10 @@ struct StepArgs {
   // ring rows are those of slot slot[b] (int32, clamped to [0, n_slots));
   // nullptr: slot b
   const uint8_t* slot; uint32_t sl_s; int32_t n_slots;
-  // device word counting bounded waits that gave up (status_word())
+  // device word counting bounded waits that gave up (status_word()), and
+  // the poll budget of every bounded wait (wait_polls())
   uint32_t* status;
+  uint32_t wait_polls;
 };
 
 struct PrepArgs {
@@ -177,6 +180,10 @@ int32_t decode_lds_bytes(int32_t units, int32_t row_waves, int32_t vblocks);
 // up (nullptr if the symbol cannot be resolved), and its host read-out
 uint32_t* status_word();
 int read_status(uint32_t* count, bool reset);
+// poll budget of the kernels' bounded waits (kWaitPolls until the host sets
+// another with gdnr_set_wait_polls; process-wide)
+uint32_t wait_polls();
+uint32_t set_wait_polls(uint32_t polls);
 int device_cus();
 // The split replay's device array for gdnr_replay_fp8_split_noalloc (T_0 and
 // the coefficients, packed; 3 MiB per GPU: B*HV <= 4096 at K = 128 with a

@@ -1,5 +1,6 @@
 // gdnr_status.hip -- the device word through which kernels report bounded
-// waits that gave up (an LDS flag never raised), and its host read-out; the
+// waits that gave up (an LDS flag never raised), its host read-out and the
+// waits' poll budget; the
 // device array of the split replay entry point that allocates nothing; the
 // compute-unit count of the current device.
 //
@@ -8,6 +9,8 @@
 // atomic; the host reads and optionally clears it with gdnr_wait_timeouts().
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include <atomic>
 
 #include "gdnr_internal.h"
 
@@ -30,6 +33,16 @@ uint32_t* status_word() {
   }
   return g_status_ptr[dev];
 }
+
+// The poll budget of the bounded waits, read by the launchers at each
+// launch. Lowering it is a test of the give-up path: with 0 every wait
+// gives up at once, the kernels still run to their end, and the waves whose
+// waits gave up leave the checkpoint and its scales as they were.
+namespace {
+std::atomic<uint32_t> g_wait_polls{kWaitPolls};
+}  // namespace
+uint32_t wait_polls() { return g_wait_polls.load(std::memory_order_relaxed); }
+uint32_t set_wait_polls(uint32_t polls) { return g_wait_polls.exchange(polls, std::memory_order_relaxed); }
 
 int read_status(uint32_t* count, bool reset) {
   uint32_t* p = status_word();

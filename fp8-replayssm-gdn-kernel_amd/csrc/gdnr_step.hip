@@ -179,7 +179,7 @@ __device__ __attribute__((noinline)) void flush_vblocks(
     uint8_t* f_ck_rows, uint8_t* f_scale_hv, uint8_t* f_out_rows, uint32_t f_ck_v, uint32_t f_sc_v, int32_t f_sc_row0,
     float f_out_scale, int32_t f_lds_k, int32_t f_lds_knew, int32_t f_lds_q, int32_t f_lds_r, int32_t f_lds_fac,
     int32_t f_lds_lam, int32_t f_lds_kt, int32_t f_vbuf, int32_t f_lds_xam, int32_t f_j_head, int32_t f_n,
-    int32_t f_pos, int32_t f_mm, int32_t f_nvb, uint32_t* f_status, bool f_ok) {
+    int32_t f_pos, int32_t f_mm, int32_t f_nvb, uint32_t* f_status, uint32_t f_polls, bool f_ok) {
   FlushArgs f{f_ck_rows, f_scale_hv, f_out_rows, f_ck_v,  f_sc_v,    f_sc_row0, f_out_scale, f_lds_k,
               f_lds_knew, f_lds_q,   f_lds_r,  f_lds_fac, f_lds_lam, f_lds_kt,  f_vbuf,      f_lds_xam,
               f_j_head,   f_n,       f_pos,    f_mm,      f_nvb};
@@ -418,14 +418,14 @@ __device__ __attribute__((noinline)) void flush_vblocks(
       // other wave posts every vblock before it waits for this one)
       __hip_atomic_store(xam_mine + p, (int)(amb | 0x80000000u), __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
       uint32_t other = 0;
-      int it = 0;
-      for (; it < (1 << 22); ++it) {
+      uint32_t it = 0;
+      for (; it < f_polls; ++it) {
         other = (uint32_t)__builtin_amdgcn_readfirstlane(
             __hip_atomic_load(xam_other + p, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP));
         if (other >> 31) break;
         __builtin_amdgcn_s_sleep(1);
       }
-      if (it == (1 << 22)) {
+      if (it == f_polls) {
         if (lane == 0 && f_status) atomicAdd(f_status, 1u);
         f_ok = false;
       }
@@ -566,7 +566,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
   uint8_t* out_rows = a.out + (b * a.o_b + hv * a.o_h + (v0 + r0) * ES);
   // wait for this head's lead (bounded: the lead always publishes)
   bool waits_ok = true;
-  auto await_coefficients = [&]() { waits_ok = wait_flag(flags + j_head, a.status) && waits_ok; };
+  auto await_coefficients = [&]() { waits_ok = wait_flag(flags + j_head, a.status, a.wait_polls) && waits_ok; };
   // Ring append of the new token (full contract): its v rows from this
   // wave's LDS copy, its gates, and (streamer 0 of the key head's first
   // workgroup) q (output) and k from what the lead left in LDS. Issued after
@@ -673,7 +673,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
       if (on && lane == pos) gb = make_float2(expf(gate_new), beta_new);
     }
     // the other leads' shares of the k ring (bounded waits: every lead raises its flag)
-    for (int jj = 0; jj < a.gw; ++jj) waits_ok = wait_flag(flags + a.gw + jj, a.status) && waits_ok;
+    for (int jj = 0; jj < a.gw; ++jj) waits_ok = wait_flag(flags + a.gw + jj, a.status, a.wait_polls) && waits_ok;
 
     // Gram of the slot rows Y = [slots 0..15, q, new k]: D00 = slots x slots,
     // D01 = slots x [q, new k], D11 = [q, new k] x [q, new k], from one read of
@@ -890,7 +890,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
     // a flush splits every vblock of the head between the two waves of the
     // head: the lead takes the upper 16 rows once the streamer's copy of the
     // v rows is in LDS (bounded wait: the streamer always raises the flag)
-    waits_ok = wait_flag(flags + 2 * a.gw + j, a.status) && waits_ok;
+    waits_ok = wait_flag(flags + 2 * a.gw + j, a.status, a.wait_polls) && waits_ok;
   }
 
   // ---- streamer of head j_head ---------------------------------------------------
@@ -900,7 +900,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
     // stream. A replay holds its checkpoint rows in registers; a flush reads
     // them one vblock at a time in section 7 (its registers go to the rebuild).
     request_meta();
-    for (int jj = 0; jj < a.gw; ++jj) waits_ok = wait_flag(flags + a.gw + jj, a.status) && waits_ok;
+    for (int jj = 0; jj < a.gw; ++jj) waits_ok = wait_flag(flags + a.gw + jj, a.status, a.wait_polls) && waits_ok;
     read_meta();
     // v rows of head j first (a replay folds them into w before its matvec):
     // chunk c = 64 i + lane holds rows
@@ -1050,7 +1050,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
   flush_vblocks<Act, NCH>(ck_rows, scale_hv, out_rows, a.ck_v, a.sc_v, (v0 + r0) / kVBlock, a.out_scale, a.lds_k,
                           a.lds_knew, a.lds_q, a.lds_r, a.lds_fac, a.lds_lam, a.lds_kt, (int32_t)(vbuf - lds),
                           a.lds_flag + 4 * (5 * a.gw + 2 * kMaxVBlocks * j_head), j_head, n, pos,
-                          head_lead ? 1 : 0, NVB, a.status, waits_ok);
+                          head_lead ? 1 : 0, NVB, a.status, a.wait_polls, waits_ok);
   if (__builtin_amdgcn_readfirstlane((int)head_lead) == 0) append_token();
 }
 

@@ -92,6 +92,10 @@ def load_library(path: Path | None = None) -> ctypes.CDLL:
     lib.gdnr_abi_version.argtypes = []
     lib.gdnr_wait_timeouts.restype = ctypes.c_int
     lib.gdnr_wait_timeouts.argtypes = [ctypes.POINTER(ctypes.c_uint32), ctypes.c_int32]
+    lib.gdnr_set_wait_polls.restype = ctypes.c_uint32
+    lib.gdnr_set_wait_polls.argtypes = [ctypes.c_uint32]
+    lib.gdnr_decode_plan.restype = ctypes.c_int
+    lib.gdnr_decode_plan.argtypes = [ctypes.c_int32] * 6 + [ctypes.POINTER(ctypes.c_int32)]
     for name, (n_tensors, n_ints, *n_floats) in ENTRY_POINTS.items():
         fn = getattr(lib, name)
         fn.restype = ctypes.c_int
@@ -141,11 +145,36 @@ def current_stream(device: torch.device) -> int:
 def wait_timeouts(reset: bool = False) -> int:
     """Bounded LDS waits of the decode kernels that gave up on the current
     device since the last reset (gdnr_wait_timeouts; synchronises the device).
-    Nonzero means some step's output is meaningless and its workgroup skipped
-    its in-place checkpoint stores."""
+    Nonzero means some step's output is meaningless; the waves whose waits
+    gave up skipped their in-place checkpoint code and scale stores."""
     lib = load_library()
     count = ctypes.c_uint32(0)
     status = lib.gdnr_wait_timeouts(ctypes.byref(count), 1 if reset else 0)
     if status != 0:
         raise GdnrError(status, lib.gdnr_last_error().decode())
     return int(count.value)
+
+
+DEFAULT_WAIT_POLLS = 1 << 22
+
+
+def set_wait_polls(polls: int) -> int:
+    """Poll budget of the kernels' bounded waits for later launches
+    (process-wide; gdnr_set_wait_polls). Returns the previous budget. 0 makes
+    every wait give up at once: a test of the give-up path."""
+    return int(load_library().gdnr_set_wait_polls(int(polls)))
+
+
+def decode_plan(batch: int, heads: int, value_heads: int, value_dim: int, ring_len: int,
+                act: torch.dtype = torch.bfloat16) -> dict | None:
+    """The decode kernel's launch plan for a shape (gdnr_decode_plan), or
+    None when the shape takes another kernel."""
+    lib = load_library()
+    plan = (ctypes.c_int32 * 5)()
+    status = lib.gdnr_decode_plan(batch, heads, value_heads, value_dim, ring_len, DTYPE_CODES[act], plan)
+    if status == 2:
+        return None
+    if status != 0:
+        raise GdnrError(status, lib.gdnr_last_error().decode())
+    return {"rows_per_wave": plan[0], "waves_per_head": plan[1], "heads_per_unit": plan[2], "units": plan[3],
+            "lds_bytes": plan[4]}

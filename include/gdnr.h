@@ -81,15 +81,38 @@ int gdnr_abi_version(void);
  * Diagnostics of the decode kernels' bounded waits. Inside a workgroup the
  * waves hand the coefficient chain, the flush factors and the flush's
  * helper results to each other through LDS flags, and every such wait is
- * bounded (2^22 polls). A wait that gives up adds 1 to a per-device status
- * word; the wave then goes on with whatever the LDS holds (the step kernel
- * skips its in-place checkpoint and scale stores), so its outputs are
- * meaningless.
+ * bounded (2^22 polls by default). A wait that gives up adds 1 to a
+ * per-device status word; the wave then goes on with whatever the LDS holds,
+ * so the step's outputs are meaningless, but it skips its in-place
+ * checkpoint code and scale stores (decode and step kernels alike): a step
+ * whose waits gave up leaves the checkpoint as it was. Ring appends, which
+ * depend on no wait, are still made.
  * *count receives the current device's word; reset != 0 clears it. This
  * call synchronises the device (it copies the word to the host).
  * No counterpart in the reference (its Triton kernels have no inter-wave waits).
  */
 int gdnr_wait_timeouts(uint32_t* count, int32_t reset);
+
+/*
+ * Sets the poll budget of every bounded wait of later launches (process-wide;
+ * 4194304 = 2^22 is the default) and returns the previous budget. A budget of
+ * 0 makes every wait give up at once: a test of the give-up path, whose
+ * kernels still run to their end. No counterpart in the reference.
+ */
+uint32_t gdnr_set_wait_polls(uint32_t polls);
+
+/*
+ * The decode kernel's launch plan for a shape (the plan gdnr_replay_fp8 and
+ * gdnr_prep_replay_fp8 use for rings of <= 16 tokens and 16-bit
+ * activations): plan[0] = V-rows per row wave, plan[1] = row waves per value
+ * head, plan[2] = value heads per unit (gw), plan[3] = units per workgroup,
+ * plan[4] = LDS bytes per workgroup. GDNR_ERR_UNSUPPORTED when the shape
+ * takes another kernel. Host-only (it reads the current device's
+ * compute-unit count); tests use it to name the instantiation they cover.
+ * No counterpart in the reference (its tiling is the block_v argument).
+ */
+int gdnr_decode_plan(int32_t batch, int32_t heads, int32_t value_heads, int32_t value_dim, int32_t ring_len,
+                     int32_t act_dtype, int32_t* plan);
 
 /*
  * Measurement probe: one coalesced pass over `buffer` (any dtype,

@@ -134,18 +134,17 @@ def test_empty_batch_is_a_no_op(lib):
     assert rc == OK and msg == ""
 
 
-def test_prep_rejects_mixed_qkv_of_another_width(lib):
+def test_prep_checks_mixed_qkv_width(lib):
     B, H, HV, K, V, L = 2, 2, 4, 128, 128, 4
     args = [desc([B, 2 * H * K + HV * V - 8], BF16), desc([B, HV], BF16), desc([B, HV], BF16), desc([HV], F32),
             desc([HV], F32), desc([B], I32), desc([B, H, K], BF16), desc([B, L, H, K], BF16),
             desc([B, L, HV, V], BF16), desc([B, L, HV], BF16), desc([B, L, HV], BF16)]
     rc = lib.gdnr_prep_ring(*[ctypes.byref(a) for a in args], 1, None)
     assert rc == INVALID and "mixed_qkv" in lib.gdnr_last_error().decode()
-    # wider than 2 H K + HV V: another layer's row layout, refused (not sliced)
+    # wider than 2 H K + HV V: accepted, as by the reference (kernel:500-550
+    # reads the first 2 H K + HV V columns of each row); the A_log check below
+    # then fails on its own account
     args[0] = desc([B, 2 * H * K + HV * V + 256], BF16)
-    rc = lib.gdnr_prep_ring(*[ctypes.byref(a) for a in args], 1, None)
-    assert rc == INVALID and "2 H K + HV V" in lib.gdnr_last_error().decode()
-    args[0] = desc([B, 2 * H * K + HV * V], BF16)
     args[3] = desc([HV], BF16)                           # A_log must be f32
     rc = lib.gdnr_prep_ring(*[ctypes.byref(a) for a in args], 1, None)
     assert rc == INVALID and "a_log" in lib.gdnr_last_error().decode()
