@@ -22,12 +22,15 @@ def codes_np(payload: torch.Tensor) -> np.ndarray:
 
 
 def make_replay_case(batch, ring_len, device, seed=0, heads=16, value_heads=32, dtype=torch.bfloat16,
-                     warmup=32, valid=None, flush=None):
-    """Checkpoint (device-quantised), ring, q, valid_len, flush for one replay call."""
-    shape = synth.Shape(batch, heads, value_heads)
+                     warmup=32, valid=None, flush=None, reference_dist=False, value_dim=128):
+    """Checkpoint (device-quantised), ring, q, valid_len, flush for one replay
+    call. reference_dist: the reference's own input regime (A_log ~ U(0,1),
+    dt_bias ~ U(-4,-3): gamma ~ 0.95 per token; state 0.02 N(0,1);
+    prototype/gdn_replayssm_fp8_kernel.py:1238-1289) instead of BASELINE's."""
+    shape = synth.Shape(batch, heads, value_heads, value_dim=value_dim)
     gen = synth.generator(seed, device)
-    a_log, dt_bias = synth.gating_params(shape, gen, device)
-    state = synth.warm_state(shape, warmup, gen, device, a_log, dt_bias)
+    a_log, dt_bias = synth.gating_params(shape, gen, device, reference_dist=reference_dist)
+    state = synth.warm_state(shape, warmup, gen, device, a_log, dt_bias, reference_dist=reference_dist)
     ckpt = gk.quantize_checkpoint(state)
     q, k, v, g, beta = synth.ring_inputs(shape, ring_len, gen, device, a_log, dt_bias, dtype)
     if valid is None:

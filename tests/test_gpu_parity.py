@@ -159,6 +159,14 @@ def test_replay_full_size_config1(device):
     codes = codes_np(case["ckpt"].payload)
     assert np.mean(codes[fl] != ref_codes[fl]) < 1e-3
     assert np.array_equal(codes[~fl], case["codes0"][~fl])  # replays leave their checkpoints alone
+    # scales: the flushing sequences' within one fp16 ulp of the oracle's
+    # (the rebuilt amax may round to the neighbouring fp16 value), rarely
+    # off; the replaying sequences' untouched
+    got_s = case["ckpt"].scale.cpu().numpy()
+    ulps = np.abs(got_s[fl].view(np.uint16).astype(np.int64)
+                  - ref_scale[fl].astype(np.float16).view(np.uint16).astype(np.int64))
+    assert ulps.max() <= 1 and ulps.mean() < 0.01, (ulps.max(), ulps.mean())
+    assert np.array_equal(got_s[~fl].view(np.uint16), case["scale0"][~fl].view(np.uint16))
 
 
 @pytest.mark.parametrize("ring_len,block_v", [(4, 32), (16, 128), (64, 64)])
