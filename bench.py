@@ -19,8 +19,14 @@ Measurement:
     a coherent cycle (set = step % S, fill = (step // S) % L + 1).
   * The steps are captured into a HIP graph (torch.cuda.CUDAGraph) once per
     round of S*L steps and replayed: no host launch overhead in the timed
-    region. Timed = exactly `steps` launches (rounded up to whole rounds so
-    the cycle amortisation is exact; the JSON reports the number timed).
+    region. Timed = `steps` launches rounded up to whole rounds (so the cycle
+    amortisation is exact), and never fewer than MIN_TIMED_ROUNDS rounds
+    (>= 40 ms of launches at the headline, 3840 steps) whatever `--steps`
+    asks: a short sample measures the clock ramp, not the kernel. The JSON
+    reports the number of steps timed and the number requested.
+  * Every timed section ends by reading the device word that counts bounded
+    waits that gave up (gdnr_wait_timeouts); if any did, the step's results
+    are meaningless and the benchmark prints an error instead of a figure.
   * HIP events on the launch stream bracket the timed region; `value` is
     microseconds per decode step (lower is better).
   * roofline: algorithmic bytes per step (every compulsory tensor element
@@ -54,6 +60,22 @@ KERNEL_NAME = "decode_kernel<8, 1, true, {gate_f32}, false>"  # <tiles per row w
 CPU_SAMPLE_SECONDS = 10.0
 EXTRAS = ("core", "config1", "split", "config3", "floor")
 CPU_MAX_CYCLES = 8
+MIN_TIMED_ROUNDS = 20
+MIN_WARM_ROUNDS = 2
+
+
+class WaitTimeout(RuntimeError):
+    """A decode workgroup's bounded LDS wait gave up during a timed section."""
+
+
+def check_waits(section: str) -> None:
+    """Raise WaitTimeout if any bounded wait gave up since the last check
+    (gdnr_wait_timeouts; synchronises the device), and clear the word."""
+    import gdnr_lib
+
+    n = gdnr_lib.wait_timeouts(reset=True)
+    if n:
+        raise WaitTimeout(f"{section}: {n} bounded wait(s) gave up; the timed results are meaningless")
 
 
 def log(msg: str) -> None:
@@ -201,10 +223,13 @@ def main() -> int:
     shape = synth.Shape(B)
     traffic_shape = LayerShape(B)
     round_len = S * L
+    steps_requested = args.steps
     if args.profile:
         args.steps, args.warmup = 2 * round_len, round_len
-    rounds = max(1, math.ceil(args.steps / round_len))
-    warm_rounds = max(1, math.ceil(args.warmup / round_len))
+        rounds, warm_rounds = 2, 1
+    else:
+        rounds = max(MIN_TIMED_ROUNDS, math.ceil(args.steps / round_len))
+        warm_rounds = max(MIN_WARM_ROUNDS, math.ceil(args.warmup / round_len))
     steps = rounds * round_len
     log(f"[bench] B={B} L={L} sets={S} block_v={args.block_v} phase={args.phase}: "
         f"{rounds} timed rounds of {round_len} steps ({steps} steps), {warm_rounds} warm-up rounds")
@@ -287,6 +312,7 @@ def main() -> int:
                 else:
                     one_round()
 
+    check_waits("set-up")
     run_rounds(warm_rounds)
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -296,6 +322,7 @@ def main() -> int:
     end.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - wall0
+    check_waits("headline")
     ms_total = start.elapsed_time(end)
     us_step = ms_total * 1e3 / steps
     log(f"[bench] timed {steps} steps: {us_step:.3f} us/step (events), wall {wall * 1e6 / steps:.3f} us/step")
@@ -308,6 +335,7 @@ def main() -> int:
         "unit": "us/step",
         "n_gpus": 1,
         "steps": steps,
+        "steps_requested": steps_requested,
         "warmup": warm_rounds * round_len,
         "ms_per_step": us_step / 1e3,
         "higher_is_better": False,
@@ -371,6 +399,7 @@ def main() -> int:
         run_rounds(rounds)
         end.record(stream)
         torch.cuda.synchronize()
+        check_waits("mixed phases")
         mixed_us = start.elapsed_time(end) * 1e3 / steps
         result["mixed_phase"] = {
             "us_per_step": round(mixed_us, 4),
@@ -457,6 +486,7 @@ def _graph_us(stream, one_round, calls: int, rounds: int = 3, warm: int = 1) -> 
             graph.replay()
         end.record(stream)
     torch.cuda.synchronize()
+    check_waits("graph-timed section")
     return start.elapsed_time(end) * 1e3 / (rounds * reps * calls)
 
 
@@ -589,25 +619,23 @@ def _rel_l2(a, b) -> float:
     return float(torch.linalg.vector_norm((a - b).double()) / torch.linalg.vector_norm(b.double()))
 
 
-def config3(device, stream, windows=(4, 16, 64), B: int = 8, steps: int = 4096,
-            probes=(128, 512, 2048, 4096)) -> dict:
+def config3(device, stream, windows=(4, 16, 64), B: int = 8, steps: int = 4096) -> dict:
     """BASELINE config 3 at B=8, L in {4, 16, 64}: the full-contract step
     (fused prep + replay, flush at fill L) timed over whole ring cycles on
     enough rotating sets to exceed the Infinity Cache; then, untimed, 4096
-    steps from a zero state with fresh seeded inputs beside an fp32
-    recurrence that consumes the ring values the kernel appended. The state
-    drift follows prototype/qwen35_drift_study.py:355-418: at step s (a flush
-    step) the fp32 replay of the ring on the dequantised checkpoint it started
-    from, against the fp32 state (before the flush requantises); also the
-    requantised checkpoint's own distance."""
+    steps with fresh seeded inputs beside an fp32 recurrence that consumes
+    the ring values the kernel appended (gdn_replayssm_drift.drift_study, the
+    reference's drift metric of prototype/qwen35_drift_study.py:355-418), in
+    the reference's own input regime and in BASELINE's."""
     import torch
 
     import gdn_replayssm_fp8_kernel as gk
     import gdn_replayssm_synth as synth
+    from gdn_replayssm_drift import drift_study
 
     res = {}
     shape = synth.Shape(B)
-    HV, K, V, G = shape.value_heads, shape.key_dim, shape.value_dim, shape.group
+    HV, K, V = shape.value_heads, shape.key_dim, shape.value_dim
     bf = dict(dtype=torch.bfloat16, device=device)
     for L in windows:
         # -- timing
@@ -637,39 +665,17 @@ def config3(device, stream, windows=(4, 16, 64), B: int = 8, steps: int = 4096,
 
         us = _graph_us(stream, cycle, S * L, rounds=2)
         del sets, state
-        # -- drift (untimed)
-        gen = synth.generator(700 + L, device)
-        mixed, a_raw, b_raw = synth.raw_step_inputs(shape, steps, gen, device)
-        ck = gk.quantize_checkpoint(torch.zeros(B, HV, V, K, device=device), saturation=False)
-        q_out = torch.zeros(B, shape.heads, K, **bf)
-        k_r, v_r = torch.zeros(B, L, shape.heads, K, **bf), torch.zeros(B, L, HV, V, **bf)
-        g_r, b_r = torch.zeros(B, L, HV, **bf), torch.zeros(B, L, HV, **bf)
-        exact = torch.zeros(B, HV, V, K, device=device)
-
-        def token(S_, t):          # S <- e^g S; S += beta (v - S k) k^T (ref:155-161), fp32
-            k = k_r[:, t].float().repeat_interleave(G, dim=1)
-            S_.mul_(g_r[:, t].float().exp()[..., None, None])
-            r = (S_ * k[:, :, None, :]).sum(-1)
-            S_.add_(((v_r[:, t].float() - r) * b_r[:, t].float()[..., None])[..., None] * k[:, :, None, :])
-
+        # -- drift (untimed), in the reference's input regime and in BASELINE's
         drift = {}
-        with torch.no_grad():
-            for step in range(steps):
-                pos = step % L
-                fill = torch.full((B,), pos + 1, dtype=torch.int32, device=device)
-                start = gk.dequantize_checkpoint(ck) if step + 1 in probes else None
-                gk.gdn_prep_replay_fp8(mixed[:, step], a_raw[:, step], b_raw[:, step], a_log, dt_bias, fill - 1,
-                                       ck.payload, ck.scale, q_out, k_r, v_r, g_r, b_r, fill, fill == L)
-                token(exact, pos)
-                if start is not None:
-                    for t in range(L):
-                        token(start, t)
-                    drift[str(step + 1)] = {"state": round(_rel_l2(start, exact), 6),
-                                            "checkpoint": round(_rel_l2(gk.dequantize_checkpoint(ck), exact), 6)}
+        for regime, seed in (("reference", 700 + L), ("baseline", 800 + L)):
+            d = drift_study(L, device, steps=steps, batch=B, regime=regime, seed=seed)
+            drift[regime] = {k: (round(v, 6) if isinstance(v, float) else v) for k, v in d.items()
+                             if k not in ("regime", "window")}
         res[f"L{L}"] = {"us_per_step": round(us, 4), "drift": drift}
-        del mixed, a_raw, b_raw, exact
     res["workload"] = (f"full-contract step (fused prep + replay, flush at L), B={B}, H=16 HV=32 K=V=128, "
-                       f"timed over whole cycles on 48 rotating sets; drift over {steps} steps from a zero state")
+                       f"timed over whole cycles on 48 rotating sets; drift over {steps} steps "
+                       f"(gdn_replayssm_drift: the reference's metric, qwen35_drift_study.py:355-418) in the "
+                       f"reference's make_inputs regime from its 0.02 N(0,1) state and in BASELINE's from zero")
     return res
 
 
@@ -677,23 +683,55 @@ def stream_floor(device, stream, buffers: list) -> dict:
     """The HBM floor of the checkpoint traffic at the bench's buffer rotation:
     one coalesced pass over each set's codes in turn (gdnr_stream_probe), read
     only (what a replay must read) and read + written back in place (what a
-    flush must move)."""
+    flush must move); then the same probe swept over buffer sizes from one
+    checkpoint's codes (33.5 MB) to 1 GiB, plain and non-temporal loads, read
+    and read + write, each size on enough rotating buffers to exceed the
+    256 MB Infinity Cache. A line t = t0 + bytes / bw fitted over the sizes a
+    decode launch moves (33.5 .. 268 MB) gives the per-launch fixed cost t0
+    and the rate bw; the largest sizes run a little slower than that line."""
+    import torch
+
     import gdnr_lib
 
-    def probe(write):
+    def probe(bufs, flags):
         def one_round():
-            for buf in buffers:
-                gdnr_lib.call("gdnr_stream_probe", [buf], [write], gdnr_lib.current_stream(device))
+            for buf in bufs:
+                gdnr_lib.call("gdnr_stream_probe", [buf], [flags], gdnr_lib.current_stream(device))
         return one_round
 
     n = len(buffers)
     nbytes = buffers[0].numel() * buffers[0].element_size()
-    read_us = _graph_us(stream, probe(0), n, rounds=5)
-    rw_us = _graph_us(stream, probe(1), n, rounds=5)
-    return {"read_us": round(read_us, 4), "read_write_us": round(rw_us, 4), "bytes": nbytes,
-            "read_GBps": round(nbytes / (read_us * 1e-6) / 1e9, 1),
-            "read_write_GBps": round(2 * nbytes / (rw_us * 1e-6) / 1e9, 1),
-            "workload": f"{n} rotating checkpoint code buffers of {nbytes} bytes, one coalesced pass each"}
+    read_us = _graph_us(stream, probe(buffers, 0), n, rounds=5)
+    rw_us = _graph_us(stream, probe(buffers, 1), n, rounds=5)
+    res = {"read_us": round(read_us, 4), "read_write_us": round(rw_us, 4), "bytes": nbytes,
+           "read_GBps": round(nbytes / (read_us * 1e-6) / 1e9, 1),
+           "read_write_GBps": round(2 * nbytes / (rw_us * 1e-6) / 1e9, 1),
+           "workload": f"{n} rotating checkpoint code buffers of {nbytes} bytes, one coalesced pass each"}
+    modes = {"read": 0, "read_write": 1, "read_nt": 2, "read_write_nt": 3}
+    sizes = [nbytes << i for i in range(6)]  # 33.5 MB .. 1.07 GB at the headline shape
+    sweep = {m: [] for m in modes}
+    for size in sizes:
+        nbuf = max(2, math.ceil(768 * 2 ** 20 / size))
+        bufs = [torch.zeros(size // 16, 16, dtype=torch.uint8, device=device) for _ in range(nbuf)]
+        for m, flags in modes.items():
+            us = _graph_us(stream, probe(bufs, flags), nbuf, rounds=3)
+            moved = size * (2 if flags & 1 else 1)
+            sweep[m].append({"bytes": size, "us": round(us, 3), "GBps": round(moved / (us * 1e-6) / 1e9, 1)})
+        del bufs
+        torch.cuda.empty_cache()
+    fits = {}
+    for m, pts in sweep.items():
+        xs = [p["bytes"] * (2 if modes[m] & 1 else 1) for p in pts if p["bytes"] <= 256 * 2 ** 20]
+        ys = [p["us"] for p in pts if p["bytes"] <= 256 * 2 ** 20]
+        mx, my = sum(xs) / len(xs), sum(ys) / len(ys)
+        slope = sum((x - mx) * (y - my) for x, y in zip(xs, ys)) / sum((x - mx) ** 2 for x in xs)
+        fits[m] = {"fixed_us": round(my - slope * mx, 3), "plateau_GBps": round(1e-3 / slope, 1)}
+    res["sweep"] = sweep
+    res["fit"] = fits
+    res["sweep_workload"] = ("gdnr_stream_probe (2048 workgroups of 256 lanes, 16-byte pieces, 4 in flight per lane) "
+                             "over rotating buffers of 33.5 MB .. 1.07 GB (>= 768 MiB per rotation); fit over "
+                             "33.5 .. 268 MB: t = fixed_us + bytes moved / plateau")
+    return res
 
 
 def run_extras(names, device, stream, buffers=None) -> dict:
@@ -888,4 +926,9 @@ def calibration_copies(device) -> None:
 
 
 if __name__ == "__main__":
-    sys.exit(main())
+    try:
+        sys.exit(main())
+    except WaitTimeout as e:
+        print(f"bench.py: {e}", file=sys.stderr, flush=True)
+        print(json.dumps({"metric": METRIC, "value": None, "error": str(e)}), flush=True)
+        sys.exit(1)

@@ -1028,7 +1028,7 @@ int gdnr_dequantize_vblock32(const gdnr_tensor* payload, const gdnr_tensor* scal
   return hip_status(gdnr::launch_dequantize(q, stream));
 }
 
-int gdnr_stream_probe(const gdnr_tensor* buffer, int32_t write, void* stream) {
+int gdnr_stream_probe(const gdnr_tensor* buffer, int32_t flags, void* stream) {
   g_last_error.clear();
   if (!buffer) return fail(GDNR_ERR_INVALID_ARGUMENT, "buffer: null tensor descriptor");
   if (buffer->ndim < 1 || buffer->ndim > GDNR_MAX_DIMS)
@@ -1045,7 +1045,8 @@ int gdnr_stream_probe(const gdnr_tensor* buffer, int32_t write, void* stream) {
   if (bytes % 16) return fail(GDNR_ERR_INVALID_ARGUMENT, "buffer: %lld bytes is not a multiple of 16", (long long)bytes);
   GDNR_TRY(check_align(buffer, "buffer", 16));
   if (bytes == 0) return GDNR_OK;
-  return hip_status(gdnr::launch_stream_probe(buffer->data, bytes, write != 0, stream));
+  if (flags & ~3) return fail(GDNR_ERR_INVALID_ARGUMENT, "flags: %d (bit 0 write-back, bit 1 non-temporal)", flags);
+  return hip_status(gdnr::launch_stream_probe(buffer->data, bytes, (flags & 1) != 0, (flags & 2) != 0, stream));
 }
 
 int gdnr_bf16_step(const gdnr_tensor* state, const gdnr_tensor* q, const gdnr_tensor* k, const gdnr_tensor* v,

@@ -197,8 +197,9 @@ int launch_rmw_packed(const RmwArgs& a, int state_dt, int act_dt, bool gate_f32,
 int launch_format_quantize(const FormatArgs& a, void* stream);
 int launch_format_dequantize(const FormatArgs& a, void* stream);
 int launch_dequantize(const QuantArgs& a, void* stream);
-// coalesced stream over bytes (a multiple of 16) at buf: read only, or read and written back in place
-int launch_stream_probe(void* buf, int64_t bytes, bool write, void* stream);
+// coalesced stream over bytes (a multiple of 16) at buf: read only, or read
+// and written back in place; plain or non-temporal loads
+int launch_stream_probe(void* buf, int64_t bytes, bool write, bool nt, void* stream);
 const char* hip_error_string(int code);
 
 }  // namespace gdnr

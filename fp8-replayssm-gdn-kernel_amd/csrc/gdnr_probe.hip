@@ -1,7 +1,8 @@
 // gdnr_probe.hip -- the HBM floor of the decode path's traffic, for the
 // benchmark: a coalesced stream over one buffer (a checkpoint's codes), read
 // only (the replay's dominant traffic) or read and written back in place (the
-// flush's). Each lane moves 16 bytes per access; consecutive lanes touch
+// flush's), with plain or non-temporal loads. Each lane moves 16 bytes per
+// access; consecutive lanes touch
 // consecutive 16-byte pieces; a grid of 8 workgroups of 256 threads per
 // compute unit strides over the buffer, four accesses in flight per lane.
 #include <hip/hip_runtime.h>
@@ -14,7 +15,7 @@ namespace {
 
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
-template <bool WRITE>
+template <bool WRITE, bool NT>
 __global__ __launch_bounds__(256) void stream_probe_kernel(u32x4_t* buf, int64_t n16) {
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   const int64_t i0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -22,7 +23,11 @@ __global__ __launch_bounds__(256) void stream_probe_kernel(u32x4_t* buf, int64_t
     u32x4_t x[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k)
-      if (i + k * stride < n16) x[k] = buf[i + k * stride];
+      if (i + k * stride < n16) {
+        // (non-temporal: as the decode kernels read the checkpoint codes)
+        if constexpr (NT) x[k] = __builtin_nontemporal_load(buf + i + k * stride);
+        else x[k] = buf[i + k * stride];
+      }
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       if (i + k * stride >= n16) continue;
@@ -38,12 +43,15 @@ __global__ __launch_bounds__(256) void stream_probe_kernel(u32x4_t* buf, int64_t
 
 }  // namespace
 
-int launch_stream_probe(void* buf, int64_t bytes, bool write, void* stream) {
+int launch_stream_probe(void* buf, int64_t bytes, bool write, bool nt, void* stream) {
   hipStream_t s = (hipStream_t)stream;
   const int64_t n16 = bytes / 16;
   const unsigned grid = (unsigned)(8 * device_cus());
-  if (write) hipLaunchKernelGGL(stream_probe_kernel<true>, dim3(grid), dim3(256), 0, s, (u32x4_t*)buf, n16);
-  else hipLaunchKernelGGL(stream_probe_kernel<false>, dim3(grid), dim3(256), 0, s, (u32x4_t*)buf, n16);
+  u32x4_t* b = (u32x4_t*)buf;
+  if (write && nt) hipLaunchKernelGGL((stream_probe_kernel<true, true>), dim3(grid), dim3(256), 0, s, b, n16);
+  else if (write) hipLaunchKernelGGL((stream_probe_kernel<true, false>), dim3(grid), dim3(256), 0, s, b, n16);
+  else if (nt) hipLaunchKernelGGL((stream_probe_kernel<false, true>), dim3(grid), dim3(256), 0, s, b, n16);
+  else hipLaunchKernelGGL((stream_probe_kernel<false, false>), dim3(grid), dim3(256), 0, s, b, n16);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? 0 : (int)e;
 }

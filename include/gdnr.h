@@ -117,15 +117,17 @@ int gdnr_decode_plan(int32_t batch, int32_t heads, int32_t value_heads, int32_t 
 /*
  * Measurement probe: one coalesced pass over `buffer` (any dtype,
  * C-contiguous, 16-byte aligned, a whole number of 16-byte pieces), reading
- * it (write == 0) or reading it and writing every piece back unchanged in
- * place (write != 0). Timed by the benchmark as the HBM floor of the decode
+ * it, or (flags bit 0) reading it and writing every piece back unchanged in
+ * place; flags bit 1 makes the loads non-temporal, as the decode kernels'
+ * checkpoint loads are. Timed by the benchmark as the HBM floor of the decode
  * step's checkpoint traffic (the replay reads the codes once, the flush
- * reads and rewrites them). The buffer's contents are left unchanged.
+ * reads and rewrites them) and swept over buffer sizes for the per-launch
+ * fixed cost and the plateau. The buffer's contents are left unchanged.
  * No counterpart in the reference (its byte counts are formulas:
  * prototype/bench_gdn_replayssm.py:45-87; its bandwidth probes are
  * prototype/bench_kernel_diag.py:39-148).
  */
-int gdnr_stream_probe(const gdnr_tensor* buffer, int32_t write, void* stream);
+int gdnr_stream_probe(const gdnr_tensor* buffer, int32_t flags, void* stream);
 
 /*
  * One decode step of the replay, per sequence b:

@@ -296,3 +296,37 @@ def test_lambda_path_flush(device, ring_len):
     assert ulps.max() <= 1
     assert rel_l2(np32(out), ref) <= OUT_TOL
     assert np.array_equal(codes[~fl], case["codes0"][~fl])
+
+
+# measured on MI355X with these seeds (state drift mean / at step 4096 /
+# output drift max): L=4 0.0380 / 0.0356 / 0.0442, L=16 0.0169 / 0.0102 /
+# 0.0281, L=64 0.0064 / 0.00088 / 0.0261; the bounds sit ~25% above
+DRIFT_BOUNDS = {
+    # L: (state drift mean, state drift at 4096, output drift max)
+    4: (0.048, 0.045, 0.055),
+    16: (0.021, 0.013, 0.035),
+    64: (0.008, 0.0011, 0.033),
+}
+
+
+@pytest.mark.parametrize("window", [4, 16, 64])
+def test_long_sequence_drift(device, window):
+    """Config 3 in the reference regime (B=8, 4096 steps, fresh inputs every
+    step): the reference's drift metric (the state replayed from the device's
+    checkpoint over the ring, against the exact fp32 recurrence on the same
+    ring values, every step; gdn_replayssm_drift) stays near the levels
+    measured here and does not grow from step 512 to 4096 (measured
+    1.00 .. 1.07). Under these synthetic gates the state forgets the
+    checkpoint within a few rings, so the error each flush injects decays
+    instead of accumulating as the sqrt(flushes) law the reference found on
+    Qwen3.5's long-memory heads (REPORT.md:294-311, which would give
+    sqrt(4096 / 512) = 2.8)."""
+    from gdn_replayssm_drift import drift_study
+
+    d = drift_study(window, device, steps=4096, batch=8, regime="reference", seed=700 + window)
+    print(f"drift L={window}: " + ", ".join(f"{k} {v:.4g}" for k, v in d.items() if isinstance(v, float)))
+    mean_max, last_max, out_max = DRIFT_BOUNDS[window]
+    assert d["state_drift_mean"] < mean_max, d
+    assert d["state_drift_at_4096"] < last_max, d
+    assert d["output_drift_max"] < out_max, d
+    assert d["growth_512_to_last"] < 1.25, d
