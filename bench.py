@@ -707,7 +707,8 @@ def stream_floor(device, stream, buffers: list) -> dict:
            "read_GBps": round(nbytes / (read_us * 1e-6) / 1e9, 1),
            "read_write_GBps": round(2 * nbytes / (rw_us * 1e-6) / 1e9, 1),
            "workload": f"{n} rotating checkpoint code buffers of {nbytes} bytes, one coalesced pass each"}
-    modes = {"read": 0, "read_write": 1, "read_nt": 2, "read_write_nt": 3}
+    modes = {"read": 0, "read_write": 1, "read_nt": 2, "read_write_nt": 3, "read_chunked_nt": 6,
+             "read_chunked_tiled_nt": 14}
     sizes = [nbytes << i for i in range(6)]  # 33.5 MB .. 1.07 GB at the headline shape
     sweep = {m: [] for m in modes}
     for size in sizes:

@@ -962,9 +962,6 @@ int gdnr_prep_replay_fp8_slots(const gdnr_tensor* mixed_qkv, const gdnr_tensor* 
   GDNR_TRY(check_index_vec(flush, "flush", g.B, true));
   GDNR_TRY(check_act_tensor(out, "out", 3, {g.B, g.HV, g.V}, g.act, 2));
   GDNR_TRY(check_block_v(block_v, g));
-  if (g.L > gdnr::kStepRing)
-    return fail(GDNR_ERR_UNSUPPORTED, "state_indices: rings of at most %d tokens (got %lld)", gdnr::kStepRing,
-                (long long)g.L);
   if (g.B == 0) return GDNR_OK;
   gdnr::ReplayArgs r = {};
   fill_common(&r, g, block_v);
@@ -981,18 +978,21 @@ int gdnr_prep_replay_fp8_slots(const gdnr_tensor* mixed_qkv, const gdnr_tensor* 
   r.out = out->data;
   r.o_b = out->strides[0];
   r.o_h = out->strides[1];
-  if (decode_eligible(r, g.act)) {
-    if (!decode_offsets_fit(r, elem_size(g.act)))
-      return fail(GDNR_ERR_UNSUPPORTED,
-                  "state_indices: a slot's checkpoint and ring rows must span less than 2 GiB, and the slot "
-                  "strides 4 GiB");
+  // the decode kernel (16-bit activations, rings of <= 16 tokens; 64-bit
+  // slot bases, 32-bit offsets inside a slot), else the step kernel (rings
+  // of <= 16 tokens, tensors under 2 GiB), else the long-ring kernel (rings of
+  // up to 64 tokens, every address in 64 bits)
+  if (decode_eligible(r, g.act) && decode_offsets_fit(r, elem_size(g.act))) {
     fit_decode(&r);
     return hip_status(launch_decode(r, g.act, true, a->dtype == GDNR_DTYPE_F32, stream));
   }
-  if (!step_offsets_fit(r, elem_size(g.act)))
-    return fail(GDNR_ERR_UNSUPPORTED, "state_indices: the slot tensors must span less than 2 GiB each");
-  GDNR_TRY(fit_step(&r, elem_size(g.act)));
-  return hip_status(launch_step(r, g.act, true, a->dtype == GDNR_DTYPE_F32, stream));
+  if (r.L <= gdnr::kStepRing && step_offsets_fit(r, elem_size(g.act))) {
+    GDNR_TRY(fit_step(&r, elem_size(g.act)));
+    return hip_status(launch_step(r, g.act, true, a->dtype == GDNR_DTYPE_F32, stream));
+  }
+  fit_replay_tile(&r);
+  GDNR_TRY(fit_lds(&r, elem_size(g.act), true, true));
+  return hip_status(launch_replay(r, g.act, gdnr::kModeFused, a->dtype == GDNR_DTYPE_F32, stream));
 }
 
 int gdnr_quantize_vblock32(const gdnr_tensor* state, const gdnr_tensor* payload, const gdnr_tensor* scale,
@@ -1045,8 +1045,12 @@ int gdnr_stream_probe(const gdnr_tensor* buffer, int32_t flags, void* stream) {
   if (bytes % 16) return fail(GDNR_ERR_INVALID_ARGUMENT, "buffer: %lld bytes is not a multiple of 16", (long long)bytes);
   GDNR_TRY(check_align(buffer, "buffer", 16));
   if (bytes == 0) return GDNR_OK;
-  if (flags & ~3) return fail(GDNR_ERR_INVALID_ARGUMENT, "flags: %d (bit 0 write-back, bit 1 non-temporal)", flags);
-  return hip_status(gdnr::launch_stream_probe(buffer->data, bytes, (flags & 1) != 0, (flags & 2) != 0, stream));
+  if ((flags & ~15) || ((flags & 4) && (flags & 1)) || ((flags & 8) && !(flags & 4)))
+    return fail(GDNR_ERR_INVALID_ARGUMENT,
+                "flags: %d (bit 0 write-back, bit 1 non-temporal, bit 2 chunked read, bit 3 tiled chunks; "
+                "chunked reads only)", flags);
+  return hip_status(gdnr::launch_stream_probe(buffer->data, bytes, (flags & 1) != 0, (flags & 2) != 0,
+                                              (flags & 4) != 0, (flags & 8) != 0, stream));
 }
 
 int gdnr_bf16_step(const gdnr_tensor* state, const gdnr_tensor* q, const gdnr_tensor* k, const gdnr_tensor* v,

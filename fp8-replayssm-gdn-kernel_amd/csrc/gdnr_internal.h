@@ -198,8 +198,10 @@ int launch_format_quantize(const FormatArgs& a, void* stream);
 int launch_format_dequantize(const FormatArgs& a, void* stream);
 int launch_dequantize(const QuantArgs& a, void* stream);
 // coalesced stream over bytes (a multiple of 16) at buf: read only, or read
-// and written back in place; plain or non-temporal loads
-int launch_stream_probe(void* buf, int64_t bytes, bool write, bool nt, void* stream);
+// and written back in place; plain or non-temporal loads; chunked: read only,
+// in the decode kernel's order (a 16 KiB chunk per wave, 16 loads in flight),
+// tiled: with the decode row wave's load pattern inside each chunk
+int launch_stream_probe(void* buf, int64_t bytes, bool write, bool nt, bool chunked, bool tiled, void* stream);
 const char* hip_error_string(int code);
 
 }  // namespace gdnr

@@ -137,6 +137,17 @@ __global__ __launch_bounds__(256) void replay_kernel(const ReplayArgs a) {
   const int groups = a.HV / gw;
   const int hv0 = (wg % groups) * gw;
   const int b = wg / groups;
+  // the sequence's state (checkpoint, scales, rings) sits in slot slot[b] of
+  // a slot-indexed cache when a.slot is set (fused step only; clamped to
+  // [0, n_slots), slot 0 being the null slot), otherwise in row b; the
+  // metadata, the step inputs, q_out and out stay per batch entry b
+  int bs = b;
+  if constexpr (FUSED) {
+    if (a.slot) {
+      const int sl = uniform_i32(a.slot + (int64_t)b * a.sl_s);
+      bs = (sl >= 0 && sl < a.n_slots) ? sl : 0;
+    }
+  }
   const int h = hv0 / a.G;
   const int hv = hv0 + wave;
   const int v0 = vt * BV;
@@ -167,7 +178,7 @@ __global__ __launch_bounds__(256) void replay_kernel(const ReplayArgs a) {
         const uint8_t* qrow = (const uint8_t*)a.q + ((int64_t)b * a.q_b + (int64_t)h * a.q_h) * ES;
         dma_stage<(CPT_K + 63) / 64>(lds, a.lds_q, CPT_K, lane, [&](int c) -> const void* { return qrow + 16 * c; });
       }
-      const uint8_t* kbase = (const uint8_t*)a.k + ((int64_t)b * a.k_b + (int64_t)h * a.k_h) * ES;
+      const uint8_t* kbase = (const uint8_t*)a.k + ((int64_t)bs * a.k_b + (int64_t)h * a.k_h) * ES;
       dma_stage<MAXI_K>(lds, a.lds_k, n * CPT_K, lane, [&](int c) -> const void* {
         const int t = c / CPT_K;
         if (t == pos) return nullptr;
@@ -180,7 +191,7 @@ __global__ __launch_bounds__(256) void replay_kernel(const ReplayArgs a) {
     dma_stage<1>(lds, a.lds_t + wave * K * 4, K * 4 / 16, lane, [&](int c) -> const void* { return tqrow + 16 * c; });
   }
   {
-    const uint8_t* vbase = (const uint8_t*)a.v + ((int64_t)b * a.v_b + (int64_t)hv * a.v_h + v0) * ES;
+    const uint8_t* vbase = (const uint8_t*)a.v + ((int64_t)bs * a.v_b + (int64_t)hv * a.v_h + v0) * ES;
     dma_stage<MAXI_V>(lds, a.lds_v + wave * a.L * BV * ES, n * CPT_V, lane, [&](int c) -> const void* {
       const int t = c / CPT_V;
       if (t == pos) return nullptr;
@@ -201,8 +212,8 @@ __global__ __launch_bounds__(256) void replay_kernel(const ReplayArgs a) {
   const int gb_slot = gb_t < a.L ? gb_t : a.L - 1;
   typename Act::Bits g_bits = 0, beta_bits = 0;
   if constexpr (!APPLY) {
-    g_bits = Act::ld_bits(a.g, (int64_t)b * a.g_b + (int64_t)gb_slot * a.g_t + (int64_t)(hv0 + gb_j) * a.g_h);
-    beta_bits = Act::ld_bits(a.beta, (int64_t)b * a.be_b + (int64_t)gb_slot * a.be_t + (int64_t)(hv0 + gb_j) * a.be_h);
+    g_bits = Act::ld_bits(a.g, (int64_t)bs * a.g_b + (int64_t)gb_slot * a.g_t + (int64_t)(hv0 + gb_j) * a.g_h);
+    beta_bits = Act::ld_bits(a.beta, (int64_t)bs * a.be_b + (int64_t)gb_slot * a.be_t + (int64_t)(hv0 + gb_j) * a.be_h);
   }
   float cval = 0.f;  // APPLY: lane t holds c_t (lanes >= n are ignored)
   if constexpr (APPLY) {
@@ -238,7 +249,7 @@ __global__ __launch_bounds__(256) void replay_kernel(const ReplayArgs a) {
   // ---- 3. checkpoint tile -> VGPRs (non-temporal: read once per step) ------
   GDNR_COMPILER_FENCE();
   uint4 ck[NCH];
-  uint8_t* ckp = a.ckpt + (int64_t)b * a.ck_b + (int64_t)hv * a.ck_h + (int64_t)(v0 + gm) * a.ck_v + 16 * gi;
+  uint8_t* ckp = a.ckpt + (int64_t)bs * a.ck_b + (int64_t)hv * a.ck_h + (int64_t)(v0 + gm) * a.ck_v + 16 * gi;
 #pragma unroll
   for (int j = 0; j < NCH; ++j) {
     typedef uint32_t u32x4_nt __attribute__((ext_vector_type(4)));
@@ -284,19 +295,19 @@ __global__ __launch_bounds__(256) void replay_kernel(const ReplayArgs a) {
       // append to the global ring (each V-tile writes its own v rows)
       if (vt == 0) {
         if (wave == 0) {
-          uint8_t* kr = (uint8_t*)a.k + ((int64_t)b * a.k_b + (int64_t)pos * a.k_t + (int64_t)h * a.k_h) * ES;
+          uint8_t* kr = (uint8_t*)a.k + ((int64_t)bs * a.k_b + (int64_t)pos * a.k_t + (int64_t)h * a.k_h) * ES;
           Act::st2(kr + 2 * lane * ES, k0, k1);
         }
         if (lane == 0) {
-          Act::st(a.g, (int64_t)b * a.g_b + (int64_t)pos * a.g_t + (int64_t)hv * a.g_h, gate);
-          Act::st(a.beta, (int64_t)b * a.be_b + (int64_t)pos * a.be_t + (int64_t)hv * a.be_h, bet);
+          Act::st(a.g, (int64_t)bs * a.g_b + (int64_t)pos * a.g_t + (int64_t)hv * a.g_h, gate);
+          Act::st(a.beta, (int64_t)bs * a.be_b + (int64_t)pos * a.be_t + (int64_t)hv * a.be_h, bet);
         }
       }
 #pragma unroll
       for (int r = 0; r < NVR; ++r) {
         const int e = lane + 64 * r;
         if (e < BV)
-          Act::st(a.v, (int64_t)b * a.v_b + (int64_t)pos * a.v_t + (int64_t)hv * a.v_h + v0 + e, v_raw[r]);
+          Act::st(a.v, (int64_t)bs * a.v_b + (int64_t)pos * a.v_t + (int64_t)hv * a.v_h + v0 + e, v_raw[r]);
       }
     }
     if (vt == 0 && wave == 0) {
@@ -308,7 +319,7 @@ __global__ __launch_bounds__(256) void replay_kernel(const ReplayArgs a) {
   __builtin_amdgcn_s_barrier();
 
   float* out_tq = (float*)(lds + a.lds_t) + wave * K;
-  const uint16_t* scale_hv = a.scale + (int64_t)b * a.sc_b + (int64_t)hv * a.sc_h;
+  const uint16_t* scale_hv = a.scale + (int64_t)bs * a.sc_b + (int64_t)hv * a.sc_h;
   if (!do_flush) {
     // scale of this lane's output rows: loaded now, converted after the matvec
     uint32_t sc_bits = scale_hv[(int64_t)((v0 + out_row<NCH>(gi, gm, 0)) / kVBlock) * a.sc_v];
@@ -464,7 +475,7 @@ __global__ __launch_bounds__(256) void replay_kernel(const ReplayArgs a) {
         *(uint4*)(ckp + (int64_t)(8 * (4 * p + jj)) * a.ck_v) = make_uint4(wq[0], wq[1], wq[2], wq[3]);
       }
       if (lane == 0)
-        a.scale[(int64_t)b * a.sc_b + (int64_t)hv * a.sc_h + (int64_t)(v0 / kVBlock + p) * a.sc_v] =
+        a.scale[(int64_t)bs * a.sc_b + (int64_t)hv * a.sc_h + (int64_t)(v0 / kVBlock + p) * a.sc_v] =
             __builtin_bit_cast(uint16_t, s16);
     }
   }

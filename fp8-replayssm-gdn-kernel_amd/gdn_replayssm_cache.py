@@ -40,8 +40,8 @@ class ReplaySSMCache:
                  value_dim: int = 128, dtype: torch.dtype = torch.bfloat16, device="cuda"):
         if num_slots < 1:
             raise ValueError("num_slots must be at least 1")
-        if not 1 <= window <= 16:
-            raise ValueError("the slot-indexed step takes rings of 1 to 16 tokens")
+        if not 1 <= window <= 64:
+            raise ValueError("the slot-indexed step takes rings of 1 to 64 tokens")
         if value_heads % heads or value_dim % gk.VBLOCK:
             raise ValueError("value_heads must be a multiple of heads and value_dim of 32")
         self.window, self.heads, self.value_heads = window, heads, value_heads

@@ -119,7 +119,11 @@ int gdnr_decode_plan(int32_t batch, int32_t heads, int32_t value_heads, int32_t 
  * C-contiguous, 16-byte aligned, a whole number of 16-byte pieces), reading
  * it, or (flags bit 0) reading it and writing every piece back unchanged in
  * place; flags bit 1 makes the loads non-temporal, as the decode kernels'
- * checkpoint loads are. Timed by the benchmark as the HBM floor of the decode
+ * checkpoint loads are; flags bit 2 (reads only) reads in the decode
+ * kernel's order instead of a grid-strided sweep: one workgroup of 8 waves
+ * per compute unit, each wave a contiguous 16 KiB chunk with 16 loads in
+ * flight per lane; with bit 3 as well, each chunk is read in the decode row
+ * wave's pattern (every load takes half of each of 16 rows of 128 bytes). Timed by the benchmark as the HBM floor of the decode
  * step's checkpoint traffic (the replay reads the codes once, the flush
  * reads and rewrites them) and swept over buffer sizes for the per-launch
  * fixed cost and the plateau. The buffer's contents are left unchanged.
@@ -243,8 +247,9 @@ int gdnr_prep_replay_fp8(const gdnr_tensor* mixed_qkv, const gdnr_tensor* a,
  * there and their outputs are meaningless). state_indices [B] i32 (clamped
  * on the device to [0, S), out of range -> 0); mixed_qkv, a, b, pos, q_out,
  * valid_len, flush and out are per batch entry as in gdnr_prep_replay_fp8.
- * Two batch entries must not name the same non-null slot. L <= 16; each slot
- * tensor must span less than 2 GiB.
+ * Two batch entries must not name the same non-null slot. 1 <= L <= 64, as
+ * for gdnr_prep_replay_fp8; caches of any size (slot bases and offsets are
+ * formed in 64 bits).
  * No counterpart in the reference's kernels: the slot contract is the
  * production op's (initial_state = kv_cache[1] [slots,HV,V,K],
  * ssm_state_indices with slot 0 the null block), findings.md:35-45, applied

@@ -238,7 +238,7 @@ def _slots_call(lib, args, block_v=128):
 
 
 @pytest.mark.parametrize("kwargs,code,needle", [
-    ({"L": 32}, UNSUPPORTED, "at most 16"),
+    ({"L": 65}, UNSUPPORTED, "ring length 65 outside [1, 64]"),
     ({"idx_dt": I64}, INVALID, "state_indices"),
     ({"S": 0}, INVALID, "null slot"),
 ])

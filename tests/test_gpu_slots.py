@@ -27,12 +27,14 @@ from oracle import gdn_oracle
 pytestmark = pytest.mark.gpu
 
 
-def test_slots_equal_direct_path(device):
+@pytest.mark.parametrize("L", [8, 32, 64])
+def test_slots_equal_direct_path(device, L):
     """8 sequences live in slots 9, 2, 5, 11, 1, 7, 4, 10 of a 12-slot cache;
-    the batch also carries two padding entries. 20 steps with staggered ring
-    fills (L=8, so every sequence flushes twice): every output, ring row and
-    checkpoint byte equals the direct path's on batch-ordered copies."""
-    L, B, steps = 8, 8, 20
+    the batch also carries two padding entries. 2.5 ring cycles with
+    staggered ring fills (every sequence flushes twice): every output, ring
+    row and checkpoint byte equals the direct path's on batch-ordered copies.
+    L = 8 runs the decode kernel; L = 32 and 64 the long-ring kernel."""
+    B, steps = 8, (5 * L) // 2
     shape = synth.Shape(B)
     gen = synth.generator(61, device)
     a_log, dt_bias = synth.gating_params(shape, gen, device)
@@ -91,13 +93,16 @@ def test_slots_equal_direct_path(device):
         assert torch.equal(r[0], before)
 
 
-def test_slots_beyond_4096_equal_direct_path(device):
+@pytest.mark.parametrize("L", [8, 64])
+def test_slots_beyond_4096_equal_direct_path(device, L):
     """A cache of 5000 slots (a 2.6 GB checkpoint, more than 4 GiB of ring and
     checkpoint together: every sequence's base address needs 64 bits): six
-    sequences in slots 4999, 4097, 4096, 2049, 4998 and 17, 10 steps with
-    staggered fills (L=8, so some flush): outputs, ring rows and checkpoint
-    bytes equal the direct path's on batch-ordered copies, bit for bit."""
-    L, B, steps, n_slots = 8, 6, 10, 5000
+    sequences in slots 4999, 4097, 4096, 2049, 4998 and 17, L + 2 steps with
+    staggered fills (every sequence flushes): outputs, ring rows and
+    checkpoint bytes equal the direct path's on batch-ordered copies, bit
+    for bit. L = 8: the decode kernel; L = 64: the long-ring kernel (6.4 GiB
+    of cache)."""
+    B, steps, n_slots = 6, L + 2, 5000
     shape = synth.Shape(B)
     gen = synth.generator(63, device)
     a_log, dt_bias = synth.gating_params(shape, gen, device)
