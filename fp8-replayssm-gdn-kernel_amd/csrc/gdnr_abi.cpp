@@ -473,13 +473,29 @@ void fill_index(const gdnr_tensor* t, const T** p, int64_t* s) {
 // The decode kernel (gdnr_decode.hip) takes 16-bit activations, rings of up
 // to kStepRing tokens and V = 64, 128 or 256 (one wave of 64 or 128 rows per
 // value head, two of 128 rows for V = 256); gw value heads per workgroup
-// beside its chain wave. sw carries V / 64 to the launcher.
+// beside its chain wave. Rings of up to kDecodeChunks kStepRing tokens run
+// as chunks of kStepRing on V = 64 or 128 (one value head per unit, waves of
+// 64 rows). sw carries V / 64 to the launcher.
 bool decode_eligible(const gdnr::ReplayArgs& a, int act) {
-  return (act == GDNR_DTYPE_BF16 || act == GDNR_DTYPE_F16) && a.L <= gdnr::kStepRing &&
-         (a.V == 64 || a.V == 128 || a.V == 256);
+  if (act != GDNR_DTYPE_BF16 && act != GDNR_DTYPE_F16) return false;
+  if (a.L <= gdnr::kStepRing) return a.V == 64 || a.V == 128 || a.V == 256;
+  // (a ring of chunks: while its workgroups, two per compute unit, run in
+  // one round; larger batches run faster on the long-ring kernel)
+  return a.L <= gdnr::kDecodeChunks * gdnr::kStepRing && (a.V == 64 || a.V == 128) &&
+         (int64_t)a.B * a.H * a.G <= 2 * (int64_t)gdnr::device_cus();
 }
 void fit_decode(gdnr::ReplayArgs* a) {
   const int32_t cus = gdnr::device_cus();
+  if (a->L > gdnr::kStepRing) {
+    // a ring of chunks: one value head per unit and workgroup (two of which
+    // share a compute unit), waves of 64 rows
+    a->gw = 1;
+    a->nwh = a->V / 64;
+    a->sw = a->V / 64;
+    a->units = 1;
+    a->lds_bytes = gdnr::decode_lds_bytes(1, a->nwh, 2, gdnr::kDecodeChunks);
+    return;
+  }
   a->nwh = a->V == 256 ? 2 : 1;  // row waves per value head
   a->gw = a->G % 2 == 0 ? 2 : 1;  // value heads per unit (at most 2; they share the unit's chain wave)
   // small batches: one value head per unit (twice the units), and for V = 128
@@ -511,7 +527,7 @@ void fit_decode(gdnr::ReplayArgs* a) {
     }
   }
   // vblocks per row wave: V / 32 / nwh
-  a->lds_bytes = gdnr::decode_lds_bytes(a->units, a->gw * a->nwh, a->V / 32 / a->nwh);
+  a->lds_bytes = gdnr::decode_lds_bytes(a->units, a->gw * a->nwh, a->V / 32 / a->nwh, 1);
 }
 int launch_decode(const gdnr::ReplayArgs& r, int act, bool fused, bool gate_f32, void* stream) {
   gdnr::StepArgs a = make_step_args(r, elem_size(act), gate_f32 ? 4 : elem_size(act));
@@ -675,8 +691,10 @@ int gdnr_decode_plan(int32_t batch, int32_t heads, int32_t value_heads, int32_t 
   gdnr::ReplayArgs a = {};
   a.B = batch, a.H = heads, a.HV = value_heads, a.G = value_heads / heads, a.V = value_dim, a.L = ring_len;
   if (!decode_eligible(a, act_dtype))
-    return fail(GDNR_ERR_UNSUPPORTED, "no decode-kernel plan: 16-bit activations, L <= %d, V in {64, 128, 256}",
-                gdnr::kStepRing);
+    return fail(GDNR_ERR_UNSUPPORTED,
+                "no decode-kernel plan: 16-bit activations, and L <= %d with V in {64, 128, 256} or L <= %d with "
+                "V in {64, 128}",
+                gdnr::kStepRing, gdnr::kDecodeChunks * gdnr::kStepRing);
   fit_decode(&a);
   plan[0] = a.V / a.nwh;
   plan[1] = a.nwh;
@@ -712,7 +730,7 @@ int gdnr_replay_fp8(const gdnr_tensor* checkpoint, const gdnr_tensor* checkpoint
   a.out = out->data;
   a.o_b = out->strides[0];
   a.o_h = out->strides[1];
-  if (a.L <= gdnr::kStepRing && decode_eligible(a, g.act) && decode_offsets_fit(a, elem_size(g.act))) {
+  if (decode_eligible(a, g.act) && decode_offsets_fit(a, elem_size(g.act))) {
     fit_decode(&a);
     return hip_status(launch_decode(a, g.act, false, false, stream));
   }
@@ -926,7 +944,7 @@ int gdnr_prep_replay_fp8(const gdnr_tensor* mixed_qkv, const gdnr_tensor* a, con
   r.out = out->data;
   r.o_b = out->strides[0];
   r.o_h = out->strides[1];
-  if (r.L <= gdnr::kStepRing && decode_eligible(r, g.act) && decode_offsets_fit(r, elem_size(g.act))) {
+  if (decode_eligible(r, g.act) && decode_offsets_fit(r, elem_size(g.act))) {
     fit_decode(&r);
     return hip_status(launch_decode(r, g.act, true, a->dtype == GDNR_DTYPE_F32, stream));
   }
@@ -978,10 +996,10 @@ int gdnr_prep_replay_fp8_slots(const gdnr_tensor* mixed_qkv, const gdnr_tensor* 
   r.out = out->data;
   r.o_b = out->strides[0];
   r.o_h = out->strides[1];
-  // the decode kernel (16-bit activations, rings of <= 16 tokens; 64-bit
-  // slot bases, 32-bit offsets inside a slot), else the step kernel (rings
-  // of <= 16 tokens, tensors under 2 GiB), else the long-ring kernel (rings of
-  // up to 64 tokens, every address in 64 bits)
+  // the decode kernel (16-bit activations, rings of <= 16 tokens, or of
+  // <= 64 with V <= 128; 64-bit slot bases, 32-bit offsets inside a slot),
+  // else the step kernel (rings of <= 16 tokens, tensors under 2 GiB), else
+  // the long-ring kernel (rings of up to 64 tokens, every address in 64 bits)
   if (decode_eligible(r, g.act) && decode_offsets_fit(r, elem_size(g.act))) {
     fit_decode(&r);
     return hip_status(launch_decode(r, g.act, true, a->dtype == GDNR_DTYPE_F32, stream));

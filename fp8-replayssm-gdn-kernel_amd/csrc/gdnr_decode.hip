@@ -230,6 +230,10 @@ constexpr int kLDq = kLG + 1024;               // k_t . q of a full ring f32 [16
 constexpr int kLFlag = kLDq + 64;              // int [16]: the unit's flags (kFlag* below)
 constexpr int kLHeads = kLFlag + 64;           // per value head blocks
 constexpr int kFlagReady = 0;                  // the chain wave's LDS blocks are complete
+constexpr int kFlagXRows = 1;                  // (NCH > 1 replay) the X rows and the query row are in LDS
+constexpr int kFlagGram = 2;                   // (NCH > 1 replay) row waves done with their Gram groups (count)
+constexpr int kChainGroups = 2;                // (NCH > 1 replay) Gram groups c < 2 the chain wave forms
+constexpr int kGfStride = 68;                  // (NCH > 1 replay) floats per row of the ring's Gram matrix
 constexpr int kFlagVStaged = 4;                // + w: row wave w's v rows are in LDS (flush)
 constexpr int kFlagHelped = 8;                 // + w: vblocks of row wave w rebuilt by helpers (flush)
 // per value head (offsets from the head's block)
@@ -243,13 +247,45 @@ constexpr int kHR = kHM + 1024;                // f32 [16][16]: R = (I + M)^-1 (
 constexpr int kHeadLds = kHR + 1024;
 constexpr int kPartials = 2;                   // helper o partials per value head (512 bytes each, in M's area)
 static_assert(kPartials * 512 <= kHR - kHM, "the helpers' o partials must fit M's area");
+
 constexpr int kMaxDecodeHeads = 2;            // value heads per unit (gw)
 constexpr int kUnitBase = kLHeads + kMaxDecodeHeads * kHeadLds;  // LDS of one unit before its v rows
-// then per row wave: its v rows, token-major ([16][64 vb + 16] bytes), and
-// two buffers of one vblock's codes for the flush (4 blocks of 64 x 16
-// bytes): the row wave's prefetch, and a helper's
+// The layout above is that of a ring of NT tokens (one chunk). A ring of NCH
+// chunks of NT tokens (L <= 16 NCH; NCH > 1 takes one value head per unit)
+// scales every per-token block: NCH NT X rows (keys only: the query of
+// NCH > 1 stays in kLQK), K^T tiles, Gram blocks and k.q per chunk; per
+// head, NCH NT coefficients, flush factors, M and R blocks, and the chunk
+// decays lam_c (kHLam: [0] lam, [1] the T_0 rows' scale, [2 + c] lam_c).
+template <int NCH>
+struct Lay {
+  static constexpr int kLX = 0;
+  static constexpr int kLQK = kLX + NT * NCH * kXStride;
+  static constexpr int kLKT = kLQK + 512;
+  static constexpr int kLG = kLKT + NCH * 8 * 16 * 16 * 2;
+  static constexpr int kLDq = kLG + NCH * 1024;
+  static constexpr int kLFlag = kLDq + NCH * 64;
+  static constexpr int kLHeads = kLFlag + 64;
+  static constexpr int kHCoef = 0;
+  static constexpr int kHLam = kHCoef + NCH * 64;
+  static constexpr int kHFac = kHLam + (NCH == 1 ? 16 : 64);
+  static constexpr int kHT0 = kHFac + NCH * 256;
+  static constexpr int kHM = kHT0;
+  static constexpr int kHR = kHM + NCH * 1024;
+  static constexpr int kHeadLds = kHR + NCH * 1024;
+  static constexpr int kHeads = NCH == 1 ? kMaxDecodeHeads : 1;
+  static constexpr int kUnitBase = kLHeads + kHeads * kHeadLds;
+};
+static_assert(Lay<1>::kUnitBase == kUnitBase && Lay<1>::kHR == kHR && Lay<1>::kHFac == kHFac,
+              "a one-chunk ring keeps the layout above");
+// then per row wave: its v rows, token-major ([16 nch][64 vb + 16] bytes),
+// and two buffers of one vblock's codes for the flush (4 blocks of 64 x 16
+// bytes): the row wave's prefetch, and a helper's (a ring of nch > 1 chunks
+// takes no helpers: the prefetch buffer only, so that two workgroups of
+// its largest units share a compute unit)
 constexpr int kVblockBytes = 4 * 64 * 16;
-__host__ __device__ constexpr int row_wave_lds(int vb) { return kStepRing * (64 * vb + 16) + 2 * kVblockBytes; }
+__host__ __device__ constexpr int row_wave_lds(int nch, int vb) {
+  return NT * nch * (64 * vb + 16) + (nch == 1 ? 2 : 1) * kVblockBytes;
+}
 // Vblocks of each row wave of a flushing unit that helpers rebuild (the
 // last ones), given nhelp helper waves: the smallest longest chain
 // max(vb - k, ceil(rpu k / nhelp)), at most one per helper (each helper job
@@ -269,7 +305,9 @@ __device__ __forceinline__ int helper_vblocks(int vb, int rpu, int nhelp, int nw
   }
   return kb;
 }
-__host__ __device__ constexpr int unit_lds(int rpu, int vb) { return kUnitBase + rpu * row_wave_lds(vb); }
+__host__ __device__ constexpr int unit_lds(int nch, int rpu, int vb) {
+  return (nch == 1 ? Lay<1>::kUnitBase : nch == 2 ? Lay<2>::kUnitBase : Lay<4>::kUnitBase) + rpu * row_wave_lds(nch, vb);
+}
 
 // raw bits of a gating input (f32, or the activation dtype) and their value
 template <bool GATE_F32>
@@ -292,11 +330,17 @@ __device__ __forceinline__ float gate_value(uint32_t bits) {
 // (gfx950 kernarg preload, the build's -amdgpu-kernarg-preload-count): the
 // first requests of every wave issue before any scalar load returns.
 // Everything else comes from the StepArgs block.
-template <int TPW, int NWH, bool FUSED, bool GATE_F32, bool SLOTS>
+template <int TPW, int NWH, int NCH, bool FUSED, bool GATE_F32, bool SLOTS>
 __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void decode_kernel(
     uint8_t* ckpt, uint8_t* kring, uint32_t ck_b, uint32_t ck_h, uint32_t ck_v, uint32_t k_b, uint32_t k_t,
     uint32_t k_h, int32_t L, int32_t G, int32_t shape, const StepArgs a) {
   constexpr int ES = 2;
+  // the LDS layout of an NCH-chunk ring (these shadow the one-chunk names)
+  using LY = Lay<NCH>;
+  constexpr int kLX = LY::kLX, kLQK = LY::kLQK, kLKT = LY::kLKT, kLG = LY::kLG, kLDq = LY::kLDq;
+  constexpr int kLFlag = LY::kLFlag, kLHeads = LY::kLHeads, kHCoef = LY::kHCoef, kHLam = LY::kHLam;
+  constexpr int kHFac = LY::kHFac, kHT0 = LY::kHT0, kHM = LY::kHM, kHR = LY::kHR, kHeadLds = LY::kHeadLds;
+  constexpr int kUnitBase = LY::kUnitBase;
   constexpr int RPW = 16 * TPW;           // V-rows per row wave
   constexpr int VB = TPW / 2;             // vblocks (32 rows) per row wave
   constexpr int VSTRIDE = RPW * ES + 16;  // LDS bytes per token of a row wave's v rows
@@ -318,7 +362,7 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
   const int n_grp = uni(G / gw);
   const int h = uni(r / n_grp), grp = r - h * n_grp, b0 = uni((int)blockIdx.y * SP + us);
   const int hv0 = h * G + grp * gw;              // first value head of the unit
-  uint8_t* const ul = lds + u * unit_lds(rpu, TPW / 2);  // the unit's LDS block
+  uint8_t* const ul = lds + u * unit_lds(NCH, rpu, TPW / 2);  // the unit's LDS block
 
   int bs = b0;
   if constexpr (SLOTS) {
@@ -376,7 +420,8 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
   // 8 q4 + j: j < 4 the hi part, j >= 4 the lo part of column 4 q4 + (j & 3)).
   auto flush_vblock = [&](const uint8_t* uu, const uint8_t* hb, const uint8_t* vr, int nf, const u32x4_t (&c)[2][2],
                           float scp, uint8_t* rows, int p, bool st, float* op, auto&& after_pass1) -> float {
-    const float lamv = ((const float*)(hb + kHLam))[0];
+    // (lam of the whole ring; of chunk 0 for a ring of NCH > 1 chunks)
+    const float lamv = ((const float*)(hb + kHLam))[NCH == 1 ? 0 : 2];
     u32x4_t packed[2];
 #pragma unroll
     for (int ii = 0; ii < 2; ++ii) {
@@ -462,6 +507,85 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
           sv[ii][ct] = mfma16(u32x4_t{k2.x, k2.y, k2.x, k2.y}, packed[ii], s0);
         }
       }
+      if constexpr (NCH > 1) {
+        // (the codes are not needed past chunk 0)
+        after_pass1();
+        // chunks 1.. in turn, from the state so far (sv, f32), the one-chunk
+        // rebuild with S for lam scale S_0: P = X_c S^T with S as 16-bit
+        // hi + lo operands (two MFMAs per k-step), W = v - pre P,
+        // U = R_c W, U~ = post U, S <- lam_c S + K_c^T U~ (lam_c S the
+        // MFMA's accumulator input), o <- lam_c o + sum_t U~_t (k_t . q)
+#pragma unroll 1
+        for (int cc = 1; cc < NCH; ++cc) {
+          if (NT * cc >= nf) break;
+          const float lc = ((const float*)(hb + kHLam))[2 + cc];
+          u32x4_t pk2[2];
+#pragma unroll
+          for (int ii = 0; ii < 2; ++ii) {
+            f32x4_t pr = {0.f, 0.f, 0.f, 0.f};
+            int xo = kLX + (NT * cc + l16) * kXStride + 64 * q4;
+            asm volatile("" : "+v"(xo));
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+              const u32x4_t x = *(const u32x4_t*)(uu + xo + 16 * m);
+              const f32x4_t a0 = sv[ii][2 * m], a1 = sv[ii][2 * m + 1];
+              const float v8[8] = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+              uint32_t hi[4], lo[4];
+#pragma unroll
+              for (int w2 = 0; w2 < 4; ++w2) {
+                const uint32_t hb2 = act_bits(v8[2 * w2]) | (act_bits(v8[2 * w2 + 1]) << 16);
+                const float2 hv = Act::from_pair(hb2);
+                hi[w2] = hb2;
+                lo[w2] = act_bits(v8[2 * w2] - hv.x) | (act_bits(v8[2 * w2 + 1] - hv.y) << 16);
+              }
+              pr = mfma16(x, u32x4_t{hi[0], hi[1], hi[2], hi[3]}, pr);
+              pr = mfma16(x, u32x4_t{lo[0], lo[1], lo[2], lo[3]}, pr);
+            }
+            float wv[4], post[4], dqt[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int t = NT * cc + 4 * q4 + e;
+              const float4 fc = *(const float4*)(hb + kHFac + 16 * t);
+              post[e] = fc.y;
+              dqt[e] = fc.z;
+              const uint32_t vw = *(const uint32_t*)(vr + t * VSTRIDE + (32 * p + 2 * l16) * ES);
+              const float vv = act_val(ii ? (vw >> 16) : vw);
+              wv[e] = t < nf ? vv - fc.x * pr[e] : 0.f;
+            }
+            const float4 rr = *(const float4*)(hb + kHR + 1024 * cc + 4 * (l16 * NT + 4 * q4));
+            const float rrv[4] = {rr.x, rr.y, rr.z, rr.w};
+            f32x4_t uv = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) uv = __builtin_amdgcn_mfma_f32_16x16x4f32(rrv[e], wv[e], uv, 0, 0, 0);
+            float ut[4];
+            float o = lc * op[ii];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              ut[e] = uv[e] * post[e];
+              o = fmaf(ut[e], dqt[e], o);
+            }
+            op[ii] = o;
+            uint32_t h2[2], l2[2];
+#pragma unroll
+            for (int w2 = 0; w2 < 2; ++w2) {
+              h2[w2] = act_bits(ut[2 * w2]) | (act_bits(ut[2 * w2 + 1]) << 16);
+              const float2 hv = Act::from_pair(h2[w2]);
+              l2[w2] = act_bits(ut[2 * w2] - hv.x) | (act_bits(ut[2 * w2 + 1] - hv.y) << 16);
+            }
+            pk2[ii] = u32x4_t{h2[0], h2[1], l2[0], l2[1]};
+          }
+#pragma unroll
+          for (int ct = 0; ct < 8; ++ct) {
+#pragma unroll
+            for (int ii = 0; ii < 2; ++ii) {
+              const uint2 k2 = *(const uint2*)(uu + kLKT + cc * (8 * 16 * 16 * 2) +
+                                               2 * ((ct * 16 + l16) * 16 + 4 * q4));
+              const f32x4_t acc = sv[ii][ct] * lc;
+              sv[ii][ct] = mfma16(u32x4_t{k2.x, k2.y, k2.x, k2.y}, pk2[ii], acc);
+            }
+          }
+        }
+      }
 #pragma unroll
       for (int ct = 0; ct < 8; ++ct) {
 #pragma unroll
@@ -472,7 +596,7 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
         }
       }
     }
-    after_pass1();
+    if constexpr (NCH == 1) after_pass1();
     const uint32_t amb = wave_max_u32(__float_as_uint(am));
     // the reference quantiser (ref:36-37,83-99): s = amax / 448 (1 when amax
     // is not > 0); codes = e4m3fn(clamp(x / s, +-448)) with the unrounded s;
@@ -556,12 +680,23 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
     const int hvr = hv0 + jr;
     // ---- loads: the key ring in the X layout (all 16 rows; rows at or past
     // the fill are zeroed below), the metadata, the query / new-token rows,
-    // the gates (lane (t, j): token t of head j)
+    // the gates (lane (t, j): token t of head j). A ring of NCH > 1 chunks
+    // loads NCH blocks of 16 rows (chunk c row t: slot 16 c + t), and its
+    // one value head's gates by token: lane (t, q4) holds token 16 q4 + t.
     const int tl = l16 < L ? l16 : 0;
     const uint8_t* krow = sbase(kring, bs, k_b) + (h * k_h + (uint32_t)tl * k_t) + 64 * q4;
-    u32x4_t xr[4];
+    u32x4_t xr[NCH][4];
 #pragma unroll
-    for (int m = 0; m < 4; ++m) xr[m] = ld16(krow + 16 * m);
+    for (int m = 0; m < 4; ++m) xr[0][m] = ld16(krow + 16 * m);
+#pragma unroll
+    for (int c = 1; c < NCH; ++c) {
+      const int tc = NT * c + l16;
+      const uint8_t* kc = sbase(kring, bs, k_b) + (h * k_h + (uint32_t)(tc < L ? tc : 0) * k_t) + 64 * q4;
+#pragma unroll
+      for (int m = 0; m < 4; ++m) xr[c][m] = ld16(kc + 16 * m);
+    }
+    const int tk = NT * q4 + l16;           // (NCH > 1) the token of this lane's gates and chain
+    const int tg = NCH == 1 ? tl : (tk < L ? tk : 0);
     GDNR_COMPILER_FENCE();
     const MetaRaw meta = load_meta(a, b);
     MetaRaw pmeta{};
@@ -574,8 +709,8 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
     } else {
       qbits = ld32(a.q + (b * a.q_b + h * a.q_h) + 4 * lane);
     }
-    const uint32_t g_raw = *(const uint16_t*)(sbase(a.g, bs, a.g_b) + ((uint32_t)tl * a.g_t + hvr * a.g_h));
-    const uint32_t be_raw = *(const uint16_t*)(sbase(a.beta, bs, a.be_b) + ((uint32_t)tl * a.be_t + hvr * a.be_h));
+    const uint32_t g_raw = *(const uint16_t*)(sbase(a.g, bs, a.g_b) + ((uint32_t)tg * a.g_t + hvr * a.g_h));
+    const uint32_t be_raw = *(const uint16_t*)(sbase(a.beta, bs, a.be_b) + ((uint32_t)tg * a.be_t + hvr * a.be_h));
     uint32_t ab0 = 0, ab1 = 0;
     float alog = 0.f, dtb = 0.f;
     if constexpr (FUSED) {
@@ -611,11 +746,11 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
       int pn = 0, ppos;
       bool pfl = false;
       if (has_partner) decode_meta(pmeta, pn, ppos, pfl);
-      int hidx = 0, nhelp = 1;
+      int hidx = 0, nhelp = NCH == 1 ? 1 : 0;
       if (do_flush) {
         hv_unit = u;
-        nhelp = has_partner ? (pfl ? 0 : 2) : 1;
-      } else if (has_partner && pfl) {
+        if constexpr (NCH == 1) nhelp = has_partner ? (pfl ? 0 : 2) : 1;
+      } else if (NCH == 1 && has_partner && pfl) {
         hv_unit = up;
         hidx = 1;
         nhelp = 2;
@@ -639,7 +774,8 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
     };
     auto job_buf = [&](int kk, int wv) {
       const int bu = kk == 0 ? hv_unit : (hv_unit == u ? up : u);
-      return lds + bu * unit_lds(rpu, VB) + kUnitBase + wv * row_wave_lds(VB) + NT * VSTRIDE + kVblockBytes;
+      return lds + bu * unit_lds(NCH, rpu, VB) + kUnitBase + wv * row_wave_lds(NCH, VB) + NT * NCH * VSTRIDE +
+             kVblockBytes;
     };
 
     // ---- the query (and new key) rows: normalised as the preparation does
@@ -665,6 +801,7 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
       *(uint32_t*)(ul + kLQK + 4 * lane) = qw;
       *(uint32_t*)(ul + kLQK + 256 + 4 * lane) = kw;
     }
+    if constexpr (NCH == 1) {
     // ---- X rows: t < n the ring (the new token's own row at t == pos), t == n
     // the query, the rest zero (a full ring, n == 16, takes the query as a
     // block of its own: the q row of kLQK); written to LDS in row form
@@ -674,7 +811,7 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
       const int off = 64 * q4 + 16 * m;
       const u32x4_t z = {0u, 0u, 0u, 0u};
       const u32x4_t qv = *(const u32x4_t*)(ul + kLQK + off);
-      u32x4_t x = l16 < n ? xr[m] : (l16 == n ? qv : z);
+      u32x4_t x = l16 < n ? xr[0][m] : (l16 == n ? qv : z);
       if constexpr (FUSED) {
         const u32x4_t kv = *(const u32x4_t*)(ul + kLQK + 256 + off);
         x = (l16 == pos && l16 < n) ? kv : x;
@@ -856,6 +993,274 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
         for (int t = 0; t < NT; ++t) Rj[t * NT + l16] = (t < n && on) ? r[t] : 0.f;
       }
     }
+    } else {
+    // ---- a ring of NCH chunks, one value head (hv0). X rows: the keys only
+    // (tokens at or past the fill zero, the new token's own row at pos),
+    // row form in LDS and the A operand in registers, per chunk. Chunks past
+    // the fill are not formed (nothing reads them), and only the chunk that
+    // holds the fill, or the new token, needs a select.
+    u32x4_t xa[NCH][4];
+    const int pc = (FUSED && pos >= 0 && pos < n) ? pos / NT : -1;  // chunk of the new token's row
+    // (the new key's row in operand form, read once: a read inside the
+    // chunk's branch would wait for it there)
+    u32x4_t kv[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+      kv[m] = FUSED ? *(const u32x4_t*)(ul + kLQK + 256 + 64 * q4 + 16 * m) : u32x4_t{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int m = 0; m < 4; ++m) asm volatile("" : "+v"(kv[m]));
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+#pragma unroll
+      for (int m = 0; m < 4; ++m) xa[c][m] = xr[c][m];  // (a chunk past the fill: its Gram is not used)
+      if (NT * c >= n) continue;
+      const int t = NT * c + l16;
+      const bool keep = t < n, isnew = c == pc && t == pos;
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const int off = 64 * q4 + 16 * m;
+        u32x4_t x = isnew ? kv[m] : xr[c][m];
+        x = keep ? x : u32x4_t{0u, 0u, 0u, 0u};
+        xa[c][m] = x;
+        *(u32x4_t*)(ul + kLX + t * kXStride + off) = x;
+      }
+    }
+    float* Gs = (float*)(ul + kLG);
+    float* Dq = (float*)(ul + kLDq);
+    // (replay) the ring's whole Gram matrix, row t at float kGfStride t: the
+    // K^T tiles' area, which only a flush uses
+    static_assert(NT * NCH * kGfStride * 4 <= kLDq - kLKT, "the full Gram must fit the K^T and Gram blocks");
+    float* Gf = (float*)(ul + kLKT);
+    if (do_flush) {
+      // Gram block of each chunk, G_c = X_c X_c^T (the chunks' products
+      // interleaved: four independent accumulations), k_t . q of every
+      // token, and the chunks' K^T operand tiles (as for one chunk)
+      f32x4_t gacc[NCH], dacc[NCH];
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) gacc[c] = dacc[c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const u32x4_t qv = *(const u32x4_t*)(ul + kLQK + 64 * q4 + 16 * m);
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+          gacc[c] = mfma16(xa[c][m], xa[c][m], gacc[c]);
+          dacc[c] = mfma16(xa[c][m], l16 == 0 ? qv : u32x4_t{0u, 0u, 0u, 0u}, dacc[c]);
+        }
+      }
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) {
+        if (NT * c >= n) continue;
+        *(float4*)(Gs + c * 256 + l16 * 16 + 4 * q4) = make_float4(gacc[c][0], gacc[c][1], gacc[c][2], gacc[c][3]);
+        if (l16 == 0) *(float4*)(Dq + NT * c + 4 * q4) = make_float4(dacc[c][0], dacc[c][1], dacc[c][2], dacc[c][3]);
+        uint16_t* kt = (uint16_t*)(ul + kLKT) + c * (8 * 16 * 16);
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          const u32x4_t x = xa[c][m];
+#pragma unroll
+          for (int j8 = 0; j8 < 8; ++j8) {
+            const uint16_t e16 = (uint16_t)((x[j8 >> 1] >> (16 * (j8 & 1))) & 0xFFFFu);
+            kt[((2 * m + (j8 >> 2)) * 16 + 4 * q4 + (j8 & 3)) * 16 + l16] = e16;
+          }
+        }
+      }
+    } else {
+      // the upper tiles of the ring's Gram matrix, G[16 r + i][16 c + j]
+      // for r <= c, and k_t . q of every token: for each chunk c in the ring
+      // (group c) the products X_c X_r^T (r <= c) and X_c q interleaved.
+      // Lane (j, q4) of the tile X_c X_r^T holds G[16 c + 4 q4 + e][16 r + j],
+      // which is G[16 r + j][16 c + 4 q4 + e]: one float4 of row 16 r + j.
+      // Groups c >= kChainGroups are the row waves' (they read the X rows
+      // from LDS once the flag is up), the first ones this wave's.
+      GDNR_WAIT_LGKM0();
+      if (lane == 0)
+        __hip_atomic_store((int*)(ul + kLFlag) + kFlagXRows, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+      u32x4_t qb[4];
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const u32x4_t qv = *(const u32x4_t*)(ul + kLQK + 64 * q4 + 16 * m);
+        qb[m] = l16 == 0 ? qv : u32x4_t{0u, 0u, 0u, 0u};
+      }
+#pragma unroll
+      for (int c = 0; c < (NCH < kChainGroups ? NCH : kChainGroups); ++c) {
+        if (NT * c >= n) continue;
+        f32x4_t tacc[NCH], dacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int r = 0; r <= c; ++r) tacc[r] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+#pragma unroll
+          for (int r = 0; r <= c; ++r) tacc[r] = mfma16(xa[c][m], xa[r][m], tacc[r]);
+          dacc = mfma16(xa[c][m], qb[m], dacc);
+        }
+#pragma unroll
+        for (int r = 0; r <= c; ++r) {
+          f32x4_t g = tacc[r];
+          if (r == c) {
+            // (the diagonal tile keeps its strict upper part only: u > t)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) g[e] = 4 * q4 + e > l16 ? g[e] : 0.f;
+          }
+          *(float4*)(Gf + (NT * r + l16) * kGfStride + NT * c + 4 * q4) = make_float4(g[0], g[1], g[2], g[3]);
+        }
+        if (l16 == 0) *(float4*)(Dq + NT * c + 4 * q4) = make_float4(dacc[0], dacc[1], dacc[2], dacc[3]);
+      }
+    }
+    // lane (t, q4): token tk = 16 q4 + t, of chunk q4; its gates
+    const bool on = tk < n;
+    uint8_t* hl = ul + kLHeads;
+    float gg = act_val(g_raw);
+    float bb = act_val(be_raw);
+    if constexpr (FUSED) {
+      const float a_in = gate_value<GATE_F32>(ab0), b_in = gate_value<GATE_F32>(ab1);
+      const float x = a_in + dtb;
+      const float sp = x <= 20.0f ? logf(1.0f + expf(x)) : x;  // kernel:560, as written there
+      const float gate_new = Act::round(-expf(alog) * sp);
+      const float beta_new = Act::round(1.0f / (1.0f + expf(-b_in)));
+      if (pos >= 0 && lane == 0) {
+        *(uint16_t*)(sbase(a.g, bs, a.g_b) + ((uint32_t)pos * a.g_t + hvr * a.g_h)) = (uint16_t)act_bits(gate_new);
+        *(uint16_t*)(sbase(a.beta, bs, a.be_b) + ((uint32_t)pos * a.be_t + hvr * a.be_h)) = (uint16_t)act_bits(beta_new);
+      }
+      gg = tk == pos ? gate_new : gg;
+      bb = tk == pos ? beta_new : bb;
+    }
+    const float gam = on ? expf(gg) : 1.f;
+    const float bet = on ? bb : 0.f;
+    const float suf_in = row_suffix_prod(gam);    // within the chunk (a 16-lane row)
+    const float suf_ex = dpp_row<0x101>(suf_in, 1.f);
+    const float lamc = row_bcast<0>(suf_in);      // lam_c of the lane's chunk
+    if (!do_flush) {
+      // Replay: the one-chunk recurrence over the whole ring,
+      // s_t = beta_t (k_t . q - sum_{u > t} G_tu s_u) (tokens from the last
+      // to the first, kernel:121-173 read as in the one-chunk chain), with
+      // c_t = s_t prod_{u > t} gamma_u and T_0 = lam (q - sum_t s_t k_t).
+      // Lane tk holds row tk of G from the later chunks' tiles and the strict
+      // upper part of its own chunk's (so that its sum stops at its own
+      // token within the chunk; it takes its s at the chunk's end); s_t of
+      // each step is read from its lane (uniform) and T_0's sum accumulated
+      // with it.
+      (void)wait_count((int*)(ul + kLFlag) + kFlagGram, rpu, a.status, a.wait_polls);  // (the row waves' groups)
+      float gb[NCH][NT];
+      {
+        float4 g4[NCH][4];
+#pragma unroll
+        for (int c = 0; c < NCH; ++c)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            g4[c][i] = NT * c < n ? *(const float4*)(Gf + tk * kGfStride + NT * c + 4 * i) : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int c = 0; c < NCH; ++c)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            gb[c][4 * i] = g4[c][i].x, gb[c][4 * i + 1] = g4[c][i].y;
+            gb[c][4 * i + 2] = g4[c][i].z, gb[c][4 * i + 3] = g4[c][i].w;
+          }
+      }
+      const float bd = on ? bet * Dq[tk] : 0.f;
+      float acc = 0.f, ax = 0.f, ay = 0.f, s_mine = 0.f;
+#pragma unroll
+      for (int c = NCH - 1; c >= 0; --c) {
+        if (NT * c >= n) continue;
+        // (the chunk's 16 key words of this lane's columns, read at once: one
+        // wait for them all rather than one every step)
+        uint32_t xw[NT];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) xw[t] = *(const uint32_t*)(ul + kLX + (NT * c + t) * kXStride + 4 * lane);
+#pragma unroll
+        for (int t = 0; t < NT; ++t) asm volatile("" : "+v"(xw[t]));
+#pragma unroll
+        for (int t = NT - 1; t >= 0; --t) {
+          const float st = rdl(fmaf(-bet, acc, bd), NT * c + t);
+          acc = fmaf(gb[c][t], st, acc);
+          const float2 xv = Act::from_pair(xw[t]);
+          ax = fmaf(st, xv.x, ax);
+          ay = fmaf(st, xv.y, ay);
+        }
+        s_mine = q4 == c ? fmaf(-bet, acc, bd) : s_mine;
+      }
+      // prod_{u > t} gamma_u over the ring: within the lane's chunk, then the
+      // later chunks' lam_c
+      const float l1 = rdl(lamc, NT), l2 = NCH > 2 ? rdl(lamc, 2 * NT) : 1.f, l3 = NCH > 3 ? rdl(lamc, 3 * NT) : 1.f;
+      const float later = (q4 < 1 ? l1 : 1.f) * (q4 < 2 ? l2 : 1.f) * (q4 < 3 ? l3 : 1.f);
+      const float lam_all = rdl(lamc, 0) * l1 * l2 * l3;
+      ((float*)(hl + kHCoef))[tk] = on ? s_mine * (suf_ex * later) : 0.f;
+      const float2 qv = Act::from_pair(*(const uint32_t*)(ul + kLQK + 4 * lane));
+      const float2 T = make_float2(lam_all * (qv.x - ax), lam_all * (qv.y - ay));
+      // T_0 = T: three 16-bit rows (f16 rows scaled by a power of two)
+      float tx = T.x, ty = T.y, t0s = 1.f;
+      if constexpr (!kBF16) {
+        const float mx = __uint_as_float(wave_max_u32(max(__float_as_uint(fabsf(tx)), __float_as_uint(fabsf(ty)))));
+        if (mx > 0.f && mx < __builtin_inff()) {
+          int ex;
+          (void)frexpf(mx, &ex);
+          ex = uni(ex);
+          tx = ldexpf(tx, -ex);
+          ty = ldexpf(ty, -ex);
+          t0s = ldexpf(1.f, ex);
+        }
+      }
+      const uint32_t hw = act_bits(tx) | (act_bits(ty) << 16);
+      const float2 hv2 = Act::from_pair(hw);
+      const float rx = tx - hv2.x, ry = ty - hv2.y;
+      const uint32_t mw = act_bits(rx) | (act_bits(ry) << 16);
+      const float2 mv2 = Act::from_pair(mw);
+      const uint32_t lw = act_bits(rx - mv2.x) | (act_bits(ry - mv2.y) << 16);
+      *(uint32_t*)(hl + kHT0 + 4 * lane) = hw;
+      *(uint32_t*)(hl + kHT0 + 256 + 4 * lane) = mw;
+      *(uint32_t*)(hl + kHT0 + 512 + 4 * lane) = lw;
+      if (lane == 0) {
+        ((float*)(hl + kHLam))[0] = lam_all;
+        ((float*)(hl + kHLam))[1] = t0s;
+      }
+    } else {
+      // flush factors of every chunk at once (row q4 = chunk q4), each the
+      // one-chunk factors within its chunk: pre_t, post_t, k_t . q, lam_c,
+      // M_c and R_c = (I + M_c)^-1; the rebuild takes the chunks in turn
+      const float pre = row_prefix_prod(gam);
+      const float post = bet * suf_ex;
+      ((float4*)(hl + kHFac))[tk] = make_float4(on ? pre : 0.f, on ? post : 0.f, on ? Dq[tk] : 0.f, 0.f);
+      // the lane's Gram row within its chunk (tokens at or past the fill zero)
+      const int nc = min(max(n - NT * q4, 0), NT);
+      float gcol[NT];
+      {
+        const float4* gr = (const float4*)(Gs + q4 * 256 + l16 * 16);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float4 v4 = gr[i];
+          gcol[4 * i] = v4.x, gcol[4 * i + 1] = v4.y, gcol[4 * i + 2] = v4.z, gcol[4 * i + 3] = v4.w;
+        }
+#pragma unroll
+        for (int t = 0; t < NT; ++t) gcol[t] = t < nc ? gcol[t] : 0.f;
+      }
+      if (l16 == 0) ((float*)(hl + kHLam))[2 + q4] = lamc;
+      float* Mm = (float*)(hl + kHM) + q4 * 256;
+      {
+        float run = 1.f;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          const float gt = row_bcast_n(gam, t);
+          run = t > l16 ? run * gt : run;
+          Mm[t * NT + l16] = (l16 < t && t < nc) ? bet * run * gcol[t] : 0.f;
+        }
+      }
+      float r[NT];
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        float x = (t == l16) ? 1.f : 0.f;
+#pragma unroll
+        for (int s4 = 0; s4 < t; s4 += 4) {
+          const float4 m4 = *(const float4*)(Mm + t * NT + s4);
+          x = fmaf(-m4.x, r[s4], x);
+          if (s4 + 1 < t) x = fmaf(-m4.y, r[s4 + 1], x);
+          if (s4 + 2 < t) x = fmaf(-m4.z, r[s4 + 2], x);
+          if (s4 + 3 < t) x = fmaf(-m4.w, r[s4 + 3], x);
+        }
+        r[t] = x;
+      }
+      float* Rj = (float*)(hl + kHR) + q4 * 256;
+#pragma unroll
+      for (int t = 0; t < NT; ++t) Rj[t * NT + l16] = (t < nc && on) ? r[t] : 0.f;
+    }
+    }
     // everything is in LDS before the flag
     GDNR_WAIT_LGKM0();
     if (lane == 0)
@@ -871,7 +1276,7 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
       if (g < h_g1) dma_vblock(job_rows(g % rpu), VB - h_nh + g / rpu, job_buf(g / rpu, g % rpu));
     }
 
-      uint8_t* const uv = lds + hv_unit * unit_lds(rpu, VB);
+      uint8_t* const uv = lds + hv_unit * unit_lds(NCH, rpu, VB);
       int* const vflags = (int*)(uv + kLFlag);
       // (a wait that gives up leaves the checkpoint alone: the job's codes
       // and scale are not stored, its flags still raised)
@@ -897,7 +1302,7 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
         const uint8_t* hbv = uv + kLHeads + (wv / NWH) * kHeadLds;
         float op[2];
         const float s32 =
-            flush_vblock(uv, hbv, uv + kUnitBase + wv * row_wave_lds(VB), h_nf, c, scp, job_rows(wv), pv, h_ok, op,
+            flush_vblock(uv, hbv, uv + kUnitBase + wv * row_wave_lds(NCH, VB), h_nf, c, scp, job_rows(wv), pv, h_ok, op,
                          []() {});
         *(float2*)(hbv + kHM + 512 * (partj * h_nh + kk) + 8 * lane) = make_float2(op[0], op[1]);
         GDNR_WAIT_LGKM0();
@@ -949,14 +1354,14 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
   bool do_flush;
   read_meta(A, n, pos, do_flush);
   // (the flush: how many of its vblocks helpers take)
-  uint8_t* const vl = ul + kUnitBase + wr * row_wave_lds(VB);
-  uint8_t* const pf = vl + NT * VSTRIDE;
+  uint8_t* const vl = ul + kUnitBase + wr * row_wave_lds(NCH, VB);
+  uint8_t* const pf = vl + NT * NCH * VSTRIDE;
   int nh = 0;
   if (!do_flush) {
 #pragma unroll
     for (int i = 2; i < TPW; ++i) load_tile(i);
   } else {
-    const int nhelp = has_partner ? (partner_flushes(A) ? 0 : 2) : 1;
+    const int nhelp = NCH > 1 ? 0 : has_partner ? (partner_flushes(A) ? 0 : 2) : 1;
     nh = uni(helper_vblocks(VB, rpu, nhelp, NWH));
   }
   uint8_t* scale_hv = sbase(A.scale, bs, A.sc_b) + (hv * A.sc_h);
@@ -967,31 +1372,37 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
   // v rows of the filled slots in 16-byte pieces (CPT per token): load k of
   // lane l is token vtok(k) = k TPL + l / CPT, bytes [16 (l % CPT), +16) of
   // the wave's row block; the new token's from mixed_qkv; slots at or past
-  // the fill re-read slot 0 (dropped when used)
+  // the fill re-read slot 0 (dropped when used). A ring of NCH chunks:
+  // load k of chunk c is token 16 c + vtok(k).
   constexpr int CPT = RPW * ES / 16;  // pieces per token row block
   constexpr int TPL = 64 / CPT;       // tokens per load
-  constexpr int NVL = NT / TPL;       // loads per lane
+  constexpr int NVL = NT / TPL;       // loads per lane and chunk
   const int vpiece = lane % CPT;
   auto vtok = [&](int k) { return k * TPL + lane / CPT; };
-  u32x4_t vq[NVL];
+  u32x4_t vq[NCH][NVL];
   {
     const uint8_t* vbase = sbase(A.v, bs, A.v_b) + (hv * A.v_h + R0 * ES) + 16 * vpiece;
 #pragma unroll
-    for (int k = 0; k < NVL; ++k) {
-      const int t = vtok(k);
-      const uint8_t* src = vbase + (uint32_t)(t < n ? t : 0) * A.v_t;
-      if constexpr (FUSED)
-        if (t == pos) src = A.mixed + (b * A.mx_b + (2 * A.H * K + hv * A.V + R0) * ES) + 16 * vpiece;
-      vq[k] = *(g_u32x4*)src;
-    }
+    for (int c = 0; c < NCH; ++c)
+#pragma unroll
+      for (int k = 0; k < NVL; ++k) {
+        const int t = NT * c + vtok(k);
+        const uint8_t* src = vbase + (uint32_t)(t < n ? t : 0) * A.v_t;
+        if constexpr (FUSED)
+          if (t == pos) src = A.mixed + (b * A.mx_b + (2 * A.H * K + hv * A.V + R0) * ES) + 16 * vpiece;
+        vq[c][k] = *(g_u32x4*)src;
+      }
   }
   GDNR_COMPILER_FENCE();
   // the chain wave's LDS blocks are complete once its flag is set (a flag,
   // not a workgroup barrier: the waves of a flushing unit need not wait for
   // the other units' row waves to get their loads issued)
   // (a wait that gives up: the step's output is meaningless, and a flush
-  // stores no codes or scales)
-  const bool ready_ok = wait_flag((int*)(ul + kLFlag) + kFlagReady, A.status, A.wait_polls);
+  // stores no codes or scales.) A ring of NCH > 1 chunks, whose chain takes
+  // longer, first stages its v rows (and a replay converts its codes): the
+  // wait comes in each branch.
+  bool ready_ok = true;
+  if constexpr (NCH == 1) ready_ok = wait_flag((int*)(ul + kLFlag) + kFlagReady, A.status, A.wait_polls);
 
   // ring append of the new token's v rows (full contract; this wave's rows,
   // which no other wave reads): the lanes that loaded token pos. (The flush
@@ -1001,8 +1412,10 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
     if (pos >= 0 && !do_flush) {
       uint8_t* vw = sbase(A.v, bs, A.v_b) + ((uint32_t)pos * A.v_t + hv * A.v_h + R0 * ES) + 16 * vpiece;
 #pragma unroll
-      for (int k = 0; k < NVL; ++k)
-        if (vtok(k) == pos) *(u32x4_t*)vw = vq[k];
+      for (int c = 0; c < NCH; ++c)
+#pragma unroll
+        for (int k = 0; k < NVL; ++k)
+          if (NT * c + vtok(k) == pos) *(u32x4_t*)vw = vq[c][k];
     }
   }
   // the v rows go to LDS token-major ([16][VS] bytes; the replay once its
@@ -1010,13 +1423,16 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
   // rows of tiles (2p, 2p + 1) of token 4 q4 + e as one word
   auto stage_v = [&]() {
 #pragma unroll
-    for (int k = 0; k < NVL; ++k) *(u32x4_t*)(vl + vtok(k) * VSTRIDE + 16 * vpiece) = vq[k];
+    for (int c = 0; c < NCH; ++c)
+#pragma unroll
+      for (int k = 0; k < NVL; ++k) *(u32x4_t*)(vl + (NT * c + vtok(k)) * VSTRIDE + 16 * vpiece) = vq[c][k];
   };
-  // v of token 4 q4 + e for tile i (zero at or past the fill)
-  auto vval = [&](int i, int e) {
-    const uint32_t wv = *(const uint32_t*)(vl + (4 * q4 + e) * VSTRIDE + (32 * (i >> 1) + 2 * l16) * ES);
+  // v of token 16 c + 4 q4 + e for tile i (zero at or past the fill)
+  auto vval = [&](int i, int e, int c = 0) {
+    const int t = NT * c + 4 * q4 + e;
+    const uint32_t wv = *(const uint32_t*)(vl + t * VSTRIDE + (32 * (i >> 1) + 2 * l16) * ES);
     const float x = act_val((i & 1) ? (wv >> 16) : wv);
-    return (4 * q4 + e) < n ? x : 0.f;
+    return t < n ? x : 0.f;
   };
   uint8_t* out_rows = A.out + (b * A.o_b + hv * A.o_h + R0 * ES);
   // o of tiles 4 g .. 4 g + 3 from per-tile partials: lane (l16, q4) stores
@@ -1032,6 +1448,56 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
     // T_0 enters as the A operand rows 0 (hi), 1 (mid) and 2 (lo), the other
     // rows zero: lanes q4 == 0 get (S_0 T_0)[row] as the sum of their first
     // three outputs
+    u32x4_t cb[NCH == 1 ? 1 : TPW][4];  // (NCH > 1) the codes as B operands
+    if constexpr (NCH > 1) {
+      // the chain's Gram groups c >= kChainGroups, round robin over the row
+      // waves (as the chain forms its own: X rows from LDS as operands);
+      // first, while the codes and v rows are on their way
+      int* const gflags = (int*)(ul + kLFlag);
+      bool mine = false;
+#pragma unroll
+      for (int c = kChainGroups; c < NCH; ++c) mine = mine || ((NCH - 1 - c) % rpu == wr && NT * c < n);
+      if (mine && wait_flag(gflags + kFlagXRows, A.status, A.wait_polls)) {
+        float* Gf = (float*)(ul + kLKT);
+        float* Dq = (float*)(ul + kLDq);
+#pragma unroll
+        for (int c = kChainGroups; c < NCH; ++c) {
+          if ((NCH - 1 - c) % rpu != wr || NT * c >= n) continue;
+          f32x4_t tacc[NCH], dacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int r = 0; r <= c; ++r) tacc[r] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int m = 0; m < 4; ++m) {
+            const int off = 64 * q4 + 16 * m;
+            u32x4_t xo[NCH];
+#pragma unroll
+            for (int r = 0; r <= c; ++r) xo[r] = *(const u32x4_t*)(ul + kLX + (NT * r + l16) * kXStride + off);
+            const u32x4_t qv = *(const u32x4_t*)(ul + kLQK + off);
+#pragma unroll
+            for (int r = 0; r <= c; ++r) tacc[r] = mfma16(xo[c], xo[r], tacc[r]);
+            dacc = mfma16(xo[c], l16 == 0 ? qv : u32x4_t{0u, 0u, 0u, 0u}, dacc);
+          }
+#pragma unroll
+          for (int r = 0; r <= c; ++r) {
+            f32x4_t g = tacc[r];
+            if (r == c) {
+#pragma unroll
+              for (int e = 0; e < 4; ++e) g[e] = 4 * q4 + e > l16 ? g[e] : 0.f;
+            }
+            *(float4*)(Gf + (NT * r + l16) * kGfStride + NT * c + 4 * q4) = make_float4(g[0], g[1], g[2], g[3]);
+          }
+          if (l16 == 0) *(float4*)(Dq + NT * c + 4 * q4) = make_float4(dacc[0], dacc[1], dacc[2], dacc[3]);
+        }
+      }
+      GDNR_WAIT_LGKM0();
+      if (lane == 0) __hip_atomic_fetch_add(gflags + kFlagGram, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+      stage_v();
+#pragma unroll
+      for (int i = 0; i < TPW; ++i)
+#pragma unroll
+        for (int m = 0; m < 4; ++m) cb[i][m] = codes8(cw[i], m);
+      (void)wait_flag((int*)(ul + kLFlag) + kFlagReady, A.status, A.wait_polls);
+    }
     const uint8_t* arow = hl + kHT0 + 256 * (l16 < 3 ? l16 : 0) + 64 * q4;
     const float4 cc = *(const float4*)(hl + kHCoef + 16 * q4);
     const float t0s = ((const float*)(hl + kHLam))[1];
@@ -1047,11 +1513,12 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
 #pragma unroll
       for (int m = 0; m < 4; ++m) {
         const u32x4_t x = *(const u32x4_t*)(arow + 16 * m);
-        c = mfma16(l16 < 3 ? x : u32x4_t{0u, 0u, 0u, 0u}, codes8(cw[i], m), c);
+        if constexpr (NCH == 1) c = mfma16(l16 < 3 ? x : u32x4_t{0u, 0u, 0u, 0u}, codes8(cw[i], m), c);
+        else c = mfma16(l16 < 3 ? x : u32x4_t{0u, 0u, 0u, 0u}, cb[i][m], c);
       }
       pt[i] = (c[0] + (c[1] + c[2])) * (sct[i >> 1] * t0s);
     }
-    stage_v();
+    if constexpr (NCH == 1) stage_v();
     float part_[TPW];
 #pragma unroll
     for (int i = 0; i < TPW; ++i) {
@@ -1061,6 +1528,20 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
       wsum = fmaf(cc.w, vval(i, 3), wsum);
       part_[i] = pt[i] + wsum;
     }
+    // the other chunks' tokens (coefficients c_t of token 16 c + 4 q4 + e)
+#pragma unroll
+    for (int c = 1; c < NCH; ++c) {
+      if (NT * c >= n) break;
+      const float4 cq = *(const float4*)(hl + kHCoef + 4 * (NT * c + 4 * q4));
+#pragma unroll
+      for (int i = 0; i < TPW; ++i) {
+        float wsum = cq.x * vval(i, 0, c);
+        wsum = fmaf(cq.y, vval(i, 1, c), wsum);
+        wsum = fmaf(cq.z, vval(i, 2, c), wsum);
+        wsum = fmaf(cq.w, vval(i, 3, c), wsum);
+        part_[i] += wsum;
+      }
+    }
 #pragma unroll
     for (int g = 0; g < TPW / 4; ++g) store_out(g, part_[4 * g], part_[4 * g + 1], part_[4 * g + 2], part_[4 * g + 3]);
     return;
@@ -1069,6 +1550,7 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
   // ---- flush: the wave's vblocks in turn (flush_vblock); the last nh of
   // them rebuilt by helper waves, whose o shares come back through LDS
   stage_v();
+  if constexpr (NCH > 1) ready_ok = wait_flag((int*)(ul + kLFlag) + kFlagReady, A.status, A.wait_polls);
   int* const flags = (int*)(ul + kLFlag);
   if (lane == 0) __hip_atomic_store(flags + kFlagVStaged + wr, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
   const int own = VB - nh;
@@ -1136,12 +1618,12 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
   }
 }
 
-template <int TPW, int NWH, bool FUSED, bool GATE_F32, bool SLOTS>
+template <int TPW, int NWH, int NCH, bool FUSED, bool GATE_F32, bool SLOTS>
 int launch_variant(const StepArgs& a, hipStream_t s) {
   const int hp = a.units == 4 ? 2 : 1, sp = a.units / hp;  // as in the kernel
   const dim3 grid((unsigned)(a.H * (a.G / a.gw) / hp), (unsigned)(a.B / sp)),
       block((unsigned)(64 * a.units * (1 + a.gw * NWH)));
-  auto kernel = decode_kernel<TPW, NWH, FUSED, GATE_F32, SLOTS>;
+  auto kernel = decode_kernel<TPW, NWH, NCH, FUSED, GATE_F32, SLOTS>;
   if (a.lds_bytes > 64 * 1024) {
     const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
                                              hipFuncAttributeMaxDynamicSharedMemorySize, a.lds_bytes);
@@ -1152,13 +1634,13 @@ int launch_variant(const StepArgs& a, hipStream_t s) {
   return 0;
 }
 
-template <int TPW, int NWH>
+template <int TPW, int NWH, int NCH = 1>
 int launch_shape(const StepArgs& a, bool fused, bool gate_f32, hipStream_t s) {
-  if (!fused) return launch_variant<TPW, NWH, false, false, false>(a, s);
-  if (a.slot && gate_f32) return launch_variant<TPW, NWH, true, true, true>(a, s);
-  if (a.slot) return launch_variant<TPW, NWH, true, false, true>(a, s);
-  if (gate_f32) return launch_variant<TPW, NWH, true, true, false>(a, s);
-  return launch_variant<TPW, NWH, true, false, false>(a, s);
+  if (!fused) return launch_variant<TPW, NWH, NCH, false, false, false>(a, s);
+  if (a.slot && gate_f32) return launch_variant<TPW, NWH, NCH, true, true, true>(a, s);
+  if (a.slot) return launch_variant<TPW, NWH, NCH, true, false, true>(a, s);
+  if (gate_f32) return launch_variant<TPW, NWH, NCH, true, true, false>(a, s);
+  return launch_variant<TPW, NWH, NCH, true, false, false>(a, s);
 }
 
 }  // namespace
@@ -1166,8 +1648,8 @@ int launch_shape(const StepArgs& a, bool fused, bool gate_f32, hipStream_t s) {
 #if GDNR_ACT == 0
 // LDS bytes of the decode kernel for gw value heads (of nwh row waves each;
 // the layout is the same for both activation dtypes)
-int32_t decode_lds_bytes(int32_t units, int32_t row_waves, int32_t vblocks) {
-  return units * unit_lds(row_waves, vblocks);
+int32_t decode_lds_bytes(int32_t units, int32_t row_waves, int32_t vblocks, int32_t chunks) {
+  return units * unit_lds(chunks, row_waves, vblocks);
 }
 #endif
 
@@ -1176,7 +1658,10 @@ int GDNR_SUFFIX(launch_decode)(const StepArgs& a, bool fused, bool gate_f32, voi
   int rc;
   // V = 64 a.sw: one wave of 64 rows per value head; 128: one of 128 rows,
   // or two of 64 (small batches); 256: two of 128
-  if (a.sw == 1) rc = launch_shape<4, 1>(a, fused, gate_f32, s);
+  // (a ring longer than one chunk: waves of 64 rows, one per 64 of V)
+  if (a.L > kStepRing) rc = a.sw == 1 ? launch_shape<4, 1, kDecodeChunks>(a, fused, gate_f32, s)
+                                      : launch_shape<4, 2, kDecodeChunks>(a, fused, gate_f32, s);
+  else if (a.sw == 1) rc = launch_shape<4, 1>(a, fused, gate_f32, s);
   else if (a.sw == 2 && a.nwh == 2) rc = launch_shape<4, 2>(a, fused, gate_f32, s);
   else if (a.sw == 2) rc = launch_shape<8, 1>(a, fused, gate_f32, s);
   else rc = launch_shape<8, 2>(a, fused, gate_f32, s);

@@ -69,6 +69,7 @@ struct ReplayArgs {
 
 constexpr int32_t kMaxStepLds = 160 * 1024;  // gfx950 LDS per workgroup
 constexpr int kStepRing = 16;                // ring capacity handled by the step kernel
+constexpr int kDecodeChunks = 4;             // chunks of kStepRing tokens of the decode kernel's longest ring
 constexpr uint32_t kWaitPolls = 1u << 22;     // default poll budget of a bounded LDS wait
 
 // Argument block of the step kernel (gdnr_step.hip), built on the host from a
@@ -175,7 +176,7 @@ GDNR_DECLARE_LAUNCHERS(f32)
 // waves per value head
 int launch_decode_bf16(const StepArgs& a, bool fused, bool gate_f32, void* stream);
 int launch_decode_f16(const StepArgs& a, bool fused, bool gate_f32, void* stream);
-int32_t decode_lds_bytes(int32_t units, int32_t row_waves, int32_t vblocks);
+int32_t decode_lds_bytes(int32_t units, int32_t row_waves, int32_t vblocks, int32_t chunks);
 // the device word of the current device that counts bounded waits which gave
 // up (nullptr if the symbol cannot be resolved), and its host read-out
 uint32_t* status_word();

@@ -172,7 +172,8 @@ def flush_pattern_flushes(pattern, b):
 
 
 HEADLINE_CASES = {
-    # id: (batch, heads, value_heads, value_dim, flush pattern, expected plan (rows/wave, waves/head, gw, units))
+    # id: (batch, heads, value_heads, value_dim, flush pattern, expected plan (rows/wave, waves/head, gw, units)
+    #      [, ring length: 16 when absent])
     "B64_all_flush": (64, 16, 32, 128, "all", (128, 1, 2, 4)),
     "B64_alternate": (64, 16, 32, 128, "alternate", (128, 1, 2, 4)),
     "B512_all_flush": (512, 16, 32, 128, "all", (128, 1, 2, 1)),
@@ -183,6 +184,11 @@ HEADLINE_CASES = {
     "V64_G2_B64_alternate": (64, 16, 32, 64, "alternate", (64, 1, 2, 4)),
     "V128_G1_B16_alternate": (16, 16, 16, 128, "alternate", (64, 2, 1, 1)),
     "V128_G1_B64_alternate": (64, 16, 16, 128, "alternate", (128, 1, 1, 4)),
+    # rings of several 16-token chunks (one value head per unit, waves of 64 rows)
+    "L64_B8_all_flush": (8, 16, 32, 128, "all", (64, 2, 1, 1), 64),
+    "L64_B8_alternate": (8, 16, 32, 128, "alternate", (64, 2, 1, 1), 64),
+    "L48_V64_B8_alternate": (8, 16, 32, 64, "alternate", (64, 1, 1, 1), 48),
+    "L32_V64_B8_all_flush": (8, 16, 32, 64, "all", (64, 1, 1, 1), 32),
 }
 
 
@@ -195,11 +201,11 @@ def test_decode_flush_requantiser_bit_exact(device, case, fused):
     its codes and scales must equal the reference quantiser's on that state
     bit for bit, whichever wave (row wave, own chain wave or partner chain
     wave) rebuilt each vblock. Replaying sequences keep their codes and
-    scales untouched. L = 16, bf16."""
+    scales untouched. bf16."""
     import gdnr_lib
 
-    batch, heads, value_heads, value_dim, pattern, plan = HEADLINE_CASES[case]
-    ring = 16
+    batch, heads, value_heads, value_dim, pattern, plan, *ring = HEADLINE_CASES[case]
+    ring = ring[0] if ring else 16
     got_plan = gdnr_lib.decode_plan(batch, heads, value_heads, value_dim, ring)
     assert got_plan is not None
     assert (got_plan["rows_per_wave"], got_plan["waves_per_head"], got_plan["heads_per_unit"],

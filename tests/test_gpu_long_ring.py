@@ -1,6 +1,8 @@
 """GPU parity of the long-ring full-contract path (marked `gpu`): rings of 17
-to 64 tokens, which gdn_prep_replay_fp8 runs on the fused replay kernel
-(prep + replay or flush in one launch, csrc/gdnr_kernels.hip).
+to 64 tokens, which gdn_prep_replay_fp8 runs on the decode kernel's chunked
+path at small batches (csrc/gdnr_decode.hip, up to 16 sequences of 32 value
+heads) and on the fused replay kernel beyond (prep + replay or flush in one
+launch, csrc/gdnr_kernels.hip).
 
 The reference's full-contract cycle (prototype/bench_gdn_full_contract.py
 :225-308) over a little more than one ring with mixed ring phases, so that
@@ -45,16 +47,20 @@ def _within_bf16_ulp(got, want):
     return bool(np.all(np.abs(got - want) <= ulp)) and float(np.mean(got != want)) < 0.01
 
 
+@pytest.mark.parametrize("batch", [3, 20], ids=["decode_kernel", "replay_kernel"])
 @pytest.mark.parametrize("window", [32, 64])
-def test_long_ring_cycle_matches_oracle(device, window):
-    batch = 3
+def test_long_ring_cycle_matches_oracle(device, window, batch):
+    import gdnr_lib
+
     shape = synth.Shape(batch)
+    # (the kernel each batch is meant to run on)
+    assert (gdnr_lib.decode_plan(batch, shape.heads, shape.value_heads, shape.value_dim, window) is not None) == (batch == 3)
     gen = synth.generator(4100 + window, device)
     a_log, dt_bias = synth.gating_params(shape, gen, device)
     state = synth.warm_state(shape, 16, gen, device, a_log, dt_bias)
     steps = window + 1
     mixed, a, b = synth.raw_step_inputs(shape, steps, gen, device)
-    phase = np.array([0, window // 2, window - 1])
+    phase = np.array([0, window // 2, window - 1] + [(5 * i) % window for i in range(batch - 3)])
     ck = gk.quantize_checkpoint(state)
     codes0, scale0 = codes_np(ck.payload).copy(), ck.scale.cpu().numpy().copy()
     q_out = torch.zeros(batch, shape.heads, shape.key_dim, dtype=torch.bfloat16, device=device)

@@ -27,21 +27,25 @@ from oracle import gdn_oracle
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("L", [8, 32, 64])
-def test_slots_equal_direct_path(device, L):
-    """8 sequences live in slots 9, 2, 5, 11, 1, 7, 4, 10 of a 12-slot cache;
-    the batch also carries two padding entries. 2.5 ring cycles with
-    staggered ring fills (every sequence flushes twice): every output, ring
-    row and checkpoint byte equals the direct path's on batch-ordered copies.
-    L = 8 runs the decode kernel; L = 32 and 64 the long-ring kernel."""
-    B, steps = 8, (5 * L) // 2
+@pytest.mark.parametrize("L,nseq", [(8, 8), (32, 8), (64, 8), (64, 17)])
+def test_slots_equal_direct_path(device, L, nseq):
+    """nseq sequences live in scattered slots of a cache of nseq + 4 slots
+    (8: slots 9, 2, 5, 11, 1, 7, 4, 10 of 12); the batch also carries two
+    padding entries. 2.5 ring cycles with staggered ring fills (every
+    sequence flushes twice): every output, ring row and checkpoint byte
+    equals the direct path's on batch-ordered copies. L = 8 runs the decode
+    kernel, L = 32 and 64 with 8 sequences its chunked path (10 batch entries
+    of 32 value heads); 17 sequences at L = 64 the long-ring kernel (slots and
+    direct path both past the decode kernel's 16 sequences)."""
+    B, steps = nseq, (5 * L) // 2
     shape = synth.Shape(B)
     gen = synth.generator(61, device)
     a_log, dt_bias = synth.gating_params(shape, gen, device)
     state = synth.warm_state(shape, 32, gen, device, a_log, dt_bias)
     ck = gk.quantize_checkpoint(state)
-    slot_of = [9, 2, 5, 11, 1, 7, 4, 10]
-    cache = ReplaySSMCache(12, L, device=device)
+    rng = np.random.default_rng(nseq)
+    slot_of = [9, 2, 5, 11, 1, 7, 4, 10] if nseq == 8 else [int(x) for x in rng.permutation(np.arange(1, nseq + 4))[:nseq]]
+    cache = ReplaySSMCache(nseq + 4, L, device=device)
     for i, sl in enumerate(slot_of):
         cache.payload[sl].copy_(ck.payload[i])
         cache.scale[sl].copy_(ck.scale[i])
@@ -55,7 +59,8 @@ def test_slots_equal_direct_path(device, L):
     mixed, a, b = synth.raw_step_inputs(shape, steps, gen, device)
     pad_mixed = torch.randn(2, steps, shape.mixed_width, generator=gen, device=device).to(torch.bfloat16)
     pad_ab = torch.randn(2, steps, 32, generator=gen, device=device).to(torch.bfloat16)
-    order = [3, 0, 6, 1, 7, 2, 5, 4]  # batch entry e holds sequence order[e]
+    # batch entry e holds sequence order[e]
+    order = [3, 0, 6, 1, 7, 2, 5, 4] if nseq == 8 else [int(x) for x in rng.permutation(nseq)]
     batch_slots = [slot_of[i] for i in order[:4]] + [0] + [slot_of[i] for i in order[4:]] + [0]
     seq_of_entry = order[:4] + [None] + order[4:] + [None]
     null_before = (cache.payload[0].clone(), cache.scale[0].clone(), [r[0].clone() for r in
@@ -93,22 +98,23 @@ def test_slots_equal_direct_path(device, L):
         assert torch.equal(r[0], before)
 
 
-@pytest.mark.parametrize("L", [8, 64])
-def test_slots_beyond_4096_equal_direct_path(device, L):
+@pytest.mark.parametrize("L,nseq", [(8, 6), (64, 6), (64, 17)])
+def test_slots_beyond_4096_equal_direct_path(device, L, nseq):
     """A cache of 5000 slots (a 2.6 GB checkpoint, more than 4 GiB of ring and
     checkpoint together: every sequence's base address needs 64 bits): six
-    sequences in slots 4999, 4097, 4096, 2049, 4998 and 17, L + 2 steps with
-    staggered fills (every sequence flushes): outputs, ring rows and
-    checkpoint bytes equal the direct path's on batch-ordered copies, bit
-    for bit. L = 8: the decode kernel; L = 64: the long-ring kernel (6.4 GiB
-    of cache)."""
-    B, steps, n_slots = 6, L + 2, 5000
+    sequences in slots 4999, 4097, 4096, 2049, 4998 and 17 (17 sequences:
+    eleven more, scattered), L + 2 steps with staggered fills (every
+    sequence flushes): outputs, ring rows and checkpoint bytes equal the
+    direct path's on batch-ordered copies, bit for bit. L = 8: the decode
+    kernel; L = 64 (6.4 GiB of cache): its chunked path with 6 sequences,
+    the long-ring kernel with 17."""
+    B, steps, n_slots = nseq, L + 2, 5000
     shape = synth.Shape(B)
     gen = synth.generator(63, device)
     a_log, dt_bias = synth.gating_params(shape, gen, device)
     state = synth.warm_state(shape, 16, gen, device, a_log, dt_bias)
     ck = gk.quantize_checkpoint(state)
-    slot_of = [4999, 4097, 4096, 2049, 4998, 17]
+    slot_of = [4999, 4097, 4096, 2049, 4998, 17, 4500, 3001, 1, 4098, 4995, 2500, 100, 4200, 3999, 4001, 2][:nseq]
     cache = ReplaySSMCache(n_slots, L, device=device)
     for i, sl in enumerate(slot_of):
         cache.payload[sl].copy_(ck.payload[i])
