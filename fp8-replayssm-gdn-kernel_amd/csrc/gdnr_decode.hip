@@ -1449,6 +1449,7 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
     // rows zero: lanes q4 == 0 get (S_0 T_0)[row] as the sum of their first
     // three outputs
     u32x4_t cb[NCH == 1 ? 1 : TPW][4];  // (NCH > 1) the codes as B operands
+    uint32_t vwd[NCH][2][4];            // (NCH > 1) the v words of tiles (2 h, 2 h + 1), token 16 c + 4 q4 + e
     if constexpr (NCH > 1) {
       // the chain's Gram groups c >= kChainGroups, round robin over the row
       // waves (as the chain forms its own: X rows from LDS as operands);
@@ -1496,6 +1497,21 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
       for (int i = 0; i < TPW; ++i)
 #pragma unroll
         for (int m = 0; m < 4; ++m) cb[i][m] = codes8(cw[i], m);
+      // (the v words the sums below take, read back now: one wait here
+      // rather than one a token after the chain's flag)
+#pragma unroll
+      for (int c = 0; c < NCH; ++c)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            vwd[c][h][e] = NT * c < n ? *(const uint32_t*)(vl + (NT * c + 4 * q4 + e) * VSTRIDE + (32 * h + 2 * l16) * ES) : 0u;
+#pragma unroll
+      for (int c = 0; c < NCH; ++c)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) asm volatile("" : "+v"(vwd[c][h][e]));
       (void)wait_flag((int*)(ul + kLFlag) + kFlagReady, A.status, A.wait_polls);
     }
     const uint8_t* arow = hl + kHT0 + 256 * (l16 < 3 ? l16 : 0) + 64 * q4;
@@ -1518,28 +1534,35 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
       }
       pt[i] = (c[0] + (c[1] + c[2])) * (sct[i >> 1] * t0s);
     }
-    if constexpr (NCH == 1) stage_v();
     float part_[TPW];
-#pragma unroll
-    for (int i = 0; i < TPW; ++i) {
-      float wsum = cc.x * vval(i, 0);
-      wsum = fmaf(cc.y, vval(i, 1), wsum);
-      wsum = fmaf(cc.z, vval(i, 2), wsum);
-      wsum = fmaf(cc.w, vval(i, 3), wsum);
-      part_[i] = pt[i] + wsum;
-    }
-    // the other chunks' tokens (coefficients c_t of token 16 c + 4 q4 + e)
-#pragma unroll
-    for (int c = 1; c < NCH; ++c) {
-      if (NT * c >= n) break;
-      const float4 cq = *(const float4*)(hl + kHCoef + 4 * (NT * c + 4 * q4));
+    if constexpr (NCH == 1) {
+      stage_v();
 #pragma unroll
       for (int i = 0; i < TPW; ++i) {
-        float wsum = cq.x * vval(i, 0, c);
-        wsum = fmaf(cq.y, vval(i, 1, c), wsum);
-        wsum = fmaf(cq.z, vval(i, 2, c), wsum);
-        wsum = fmaf(cq.w, vval(i, 3, c), wsum);
-        part_[i] += wsum;
+        float wsum = cc.x * vval(i, 0);
+        wsum = fmaf(cc.y, vval(i, 1), wsum);
+        wsum = fmaf(cc.z, vval(i, 2), wsum);
+        wsum = fmaf(cc.w, vval(i, 3), wsum);
+        part_[i] = pt[i] + wsum;
+      }
+    } else {
+      // every chunk's tokens: coefficients c_t of token 16 c + 4 q4 + e
+      // (zero at or past the fill), v from the words read before the flag
+#pragma unroll
+      for (int i = 0; i < TPW; ++i) part_[i] = pt[i];
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) {
+        if (NT * c >= n) break;
+        const float4 cq = *(const float4*)(hl + kHCoef + 4 * (NT * c + 4 * q4));
+        const float cv[4] = {cq.x, cq.y, cq.z, cq.w};
+#pragma unroll
+        for (int i = 0; i < TPW; ++i)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const uint32_t w = vwd[c][i >> 1][e];
+            const float x = act_val((i & 1) ? (w >> 16) : w);
+            part_[i] = fmaf(cv[e], NT * c + 4 * q4 + e < n ? x : 0.f, part_[i]);
+          }
       }
     }
 #pragma unroll
