@@ -93,6 +93,24 @@ __device__ __forceinline__ u32x4_t codes8(const u32x4_t* c, int m) {
   const uint2 hi = codes4(w1);
   return u32x4_t{lo.x, lo.y, hi.x, hi.y};
 }
+// f32x4_to_fp8_ref with its constants formed where it runs (through empty
+// asm statements, which stay in place): the flush's rare division path uses
+// it, and constants hoisted out of the flush loop would hold registers for
+// the whole loop
+__device__ __forceinline__ uint32_t f32x4_to_fp8_ref_cold(float a, float b, float c, float d) {
+  float lim = 448.0f;
+  uint32_t k7f = 0x7Fu, kff = 0xFFu;
+  asm volatile("" : "+v"(lim), "+v"(k7f), "+v"(kff));
+  const float v[4] = {a, b, c, d};
+  float cl[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) cl[e] = (v[e] != v[e]) ? v[e] : fminf(fmaxf(v[e], -lim), lim);
+  uint32_t w = f32x4_to_fp8(cl[0], cl[1], cl[2], cl[3]);
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    if (v[e] != v[e]) w = (w & ~(kff << (8 * e))) | ((__float_as_uint(v[e]) >> 31 ? kff : k7f) << (8 * e));
+  return w;
+}
 // activation value from 16 bits
 __device__ __forceinline__ float act_val(uint32_t bits16) { return Act::from_bits(bits16 & 0xFFFFu); }
 __device__ __forceinline__ uint32_t act_bits(float x) {
@@ -635,7 +653,7 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
           qv[e] = v[e] / s32;
           __builtin_amdgcn_sched_barrier(0);
         }
-        const uint32_t wd = f32x4_to_fp8_ref(qv[0], qv[1], qv[2], qv[3]);
+        const uint32_t wd = f32x4_to_fp8_ref_cold(qv[0], qv[1], qv[2], qv[3]);
         __builtin_amdgcn_sched_barrier(0);
         return wd;
       });
