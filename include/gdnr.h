@@ -102,12 +102,14 @@ int gdnr_wait_timeouts(uint32_t* count, int32_t reset);
 uint32_t gdnr_set_wait_polls(uint32_t polls);
 
 /*
- * The decode kernel's launch plan for a shape (the plan gdnr_replay_fp8 and
- * gdnr_prep_replay_fp8 use for rings of <= 16 tokens and 16-bit
- * activations): plan[0] = V-rows per row wave, plan[1] = row waves per value
- * head, plan[2] = value heads per unit (gw), plan[3] = units per workgroup,
- * plan[4] = LDS bytes per workgroup. GDNR_ERR_UNSUPPORTED when the shape
- * takes another kernel. Host-only (it reads the current device's
+ * The decode kernel's launch plan for a shape (the plan gdnr_replay_fp8,
+ * gdnr_prep_replay_fp8 and the slot entry use with 16-bit activations: rings
+ * of <= 16 tokens with V = 64, 128 or 256, and rings of <= 64 tokens, as
+ * 16-token chunks, with V = 64 or 128 while batch * value_heads is at most
+ * twice the device's compute units): plan[0] = V-rows per row wave,
+ * plan[1] = row waves per value head, plan[2] = value heads per unit (gw),
+ * plan[3] = units per workgroup, plan[4] = LDS bytes per workgroup.
+ * GDNR_ERR_UNSUPPORTED when the shape takes another kernel. Host-only (it reads the current device's
  * compute-unit count); tests use it to name the instantiation they cover.
  * No counterpart in the reference (its tiling is the block_v argument).
  */
