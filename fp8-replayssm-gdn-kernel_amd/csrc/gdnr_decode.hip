@@ -359,6 +359,11 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
   constexpr int kLFlag = LY::kLFlag, kLHeads = LY::kLHeads, kHCoef = LY::kHCoef, kHLam = LY::kHLam;
   constexpr int kHFac = LY::kHFac, kHT0 = LY::kHT0, kHM = LY::kHM, kHR = LY::kHR, kHeadLds = LY::kHeadLds;
   constexpr int kUnitBase = LY::kUnitBase;
+  // (row waves) stage their v rows, convert their codes and read back their
+  // v words before the chain's flag, rather than after it: a ring of chunks,
+  // and the small-batch shapes (waves of 64 rows), whose launches wait on
+  // their chain; the headline shape (waves of 128 rows) waits on its stream
+  constexpr bool kEarly = NCH > 1 || TPW == 4;
   constexpr int RPW = 16 * TPW;           // V-rows per row wave
   constexpr int VB = TPW / 2;             // vblocks (32 rows) per row wave
   constexpr int VSTRIDE = RPW * ES + 16;  // LDS bytes per token of a row wave's v rows
@@ -1420,7 +1425,7 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
   // longer, first stages its v rows (and a replay converts its codes): the
   // wait comes in each branch.
   bool ready_ok = true;
-  if constexpr (NCH == 1) ready_ok = wait_flag((int*)(ul + kLFlag) + kFlagReady, A.status, A.wait_polls);
+  if constexpr (!kEarly) ready_ok = wait_flag((int*)(ul + kLFlag) + kFlagReady, A.status, A.wait_polls);
 
   // ring append of the new token's v rows (full contract; this wave's rows,
   // which no other wave reads): the lanes that loaded token pos. (The flush
@@ -1466,9 +1471,10 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
     // T_0 enters as the A operand rows 0 (hi), 1 (mid) and 2 (lo), the other
     // rows zero: lanes q4 == 0 get (S_0 T_0)[row] as the sum of their first
     // three outputs
-    u32x4_t cb[NCH == 1 ? 1 : TPW][4];  // (NCH > 1) the codes as B operands
-    uint32_t vwd[NCH][2][4];            // (NCH > 1) the v words of tiles (2 h, 2 h + 1), token 16 c + 4 q4 + e
-    if constexpr (NCH > 1) {
+    u32x4_t cb[kEarly ? TPW : 1][4];  // (kEarly) the codes as B operands
+    uint32_t vwd[NCH][2][4];          // (kEarly) the v words of tiles (2 h, 2 h + 1), token 16 c + 4 q4 + e
+    if constexpr (kEarly) {
+      if constexpr (NCH > 1) {
       // the chain's Gram groups c >= kChainGroups, round robin over the row
       // waves (as the chain forms its own: X rows from LDS as operands);
       // first, while the codes and v rows are on their way
@@ -1510,6 +1516,7 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
       }
       GDNR_WAIT_LGKM0();
       if (lane == 0) __hip_atomic_fetch_add(gflags + kFlagGram, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+      }
       stage_v();
 #pragma unroll
       for (int i = 0; i < TPW; ++i)
@@ -1547,13 +1554,13 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
 #pragma unroll
       for (int m = 0; m < 4; ++m) {
         const u32x4_t x = *(const u32x4_t*)(arow + 16 * m);
-        if constexpr (NCH == 1) c = mfma16(l16 < 3 ? x : u32x4_t{0u, 0u, 0u, 0u}, codes8(cw[i], m), c);
+        if constexpr (!kEarly) c = mfma16(l16 < 3 ? x : u32x4_t{0u, 0u, 0u, 0u}, codes8(cw[i], m), c);
         else c = mfma16(l16 < 3 ? x : u32x4_t{0u, 0u, 0u, 0u}, cb[i][m], c);
       }
       pt[i] = (c[0] + (c[1] + c[2])) * (sct[i >> 1] * t0s);
     }
     float part_[TPW];
-    if constexpr (NCH == 1) {
+    if constexpr (!kEarly) {
       stage_v();
 #pragma unroll
       for (int i = 0; i < TPW; ++i) {
@@ -1565,22 +1572,27 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
       }
     } else {
       // every chunk's tokens: coefficients c_t of token 16 c + 4 q4 + e
-      // (zero at or past the fill), v from the words read before the flag
-#pragma unroll
-      for (int i = 0; i < TPW; ++i) part_[i] = pt[i];
+      // (zero at or past the fill), v from the words read before the flag;
+      // summed as the branch above sums them (chunk 0 always, pt + its sum
+      // the only use of pt, so that the compiler contracts it the same way):
+      // either kind of launch gives the same bits
+      auto vw_val = [&](int c, int i, int e) {
+        const uint32_t w = vwd[c][i >> 1][e];
+        const float x = act_val((i & 1) ? (w >> 16) : w);
+        return NT * c + 4 * q4 + e < n ? x : 0.f;
+      };
 #pragma unroll
       for (int c = 0; c < NCH; ++c) {
-        if (NT * c >= n) break;
+        if (c > 0 && NT * c >= n) break;
         const float4 cq = *(const float4*)(hl + kHCoef + 4 * (NT * c + 4 * q4));
-        const float cv[4] = {cq.x, cq.y, cq.z, cq.w};
 #pragma unroll
-        for (int i = 0; i < TPW; ++i)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const uint32_t w = vwd[c][i >> 1][e];
-            const float x = act_val((i & 1) ? (w >> 16) : w);
-            part_[i] = fmaf(cv[e], NT * c + 4 * q4 + e < n ? x : 0.f, part_[i]);
-          }
+        for (int i = 0; i < TPW; ++i) {
+          float wsum = cq.x * vw_val(c, i, 0);
+          wsum = fmaf(cq.y, vw_val(c, i, 1), wsum);
+          wsum = fmaf(cq.z, vw_val(c, i, 2), wsum);
+          wsum = fmaf(cq.w, vw_val(c, i, 3), wsum);
+          part_[i] = c == 0 ? pt[i] + wsum : part_[i] + wsum;
+        }
       }
     }
 #pragma unroll
@@ -1591,7 +1603,7 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
   // ---- flush: the wave's vblocks in turn (flush_vblock); the last nh of
   // them rebuilt by helper waves, whose o shares come back through LDS
   stage_v();
-  if constexpr (NCH > 1) ready_ok = wait_flag((int*)(ul + kLFlag) + kFlagReady, A.status, A.wait_polls);
+  if constexpr (kEarly) ready_ok = wait_flag((int*)(ul + kLFlag) + kFlagReady, A.status, A.wait_polls);
   int* const flags = (int*)(ul + kLFlag);
   if (lane == 0) __hip_atomic_store(flags + kFlagVStaged + wr, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
   const int own = VB - nh;
