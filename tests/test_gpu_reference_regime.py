@@ -228,13 +228,19 @@ def test_long_ring_cycle(device, window):
 
 
 OTHER_SHAPES = {
-    # id: (batch, value_heads, value_dim)  (H = 16 key heads)
+    # id: (batch, value_heads, value_dim[, ring length, activation dtype])  (H = 16 key heads; L = 16, bf16 when absent)
     "V64_G2_B64": (64, 32, 64),
     "V256_G1_B32": (32, 16, 256),
     "V256_G1_B64": (64, 16, 256),
     "V256_G2_B64": (64, 32, 256),
     "V128_G1_B16": (16, 16, 128),
     "V128_G1_B64": (64, 16, 128),
+    # rings of 16-token chunks: V = 64 and 128, G = 1 and 2, up to the decode kernel's batch limit, and f16
+    "L48_V64_G2_B8": (8, 32, 64, 48),
+    "L64_V128_G1_B16": (16, 16, 128, 64),
+    "L32_V128_G2_B16": (16, 32, 128, 32),
+    "L64_V128_G2_B8_f16": (8, 32, 128, 64, torch.float16),
+    "L16_V128_G2_B8_f16": (8, 32, 128, 16, torch.float16),
 }
 
 
@@ -244,14 +250,17 @@ def test_other_decode_shapes(device, case_id):
     small and large batches), alternate sequences flushing so that partner
     units help: outputs vs the fp64 oracle, codes to rounding-boundary flips,
     scales within one fp16 ulp, replaying sequences untouched."""
-    batch, value_heads, value_dim = OTHER_SHAPES[case_id]
-    assert gdnr_lib.decode_plan(batch, H, value_heads, value_dim, 16) is not None
-    valid = np.where(np.arange(batch) % 2 == 0, 16, 1 + np.arange(batch) % 15).astype(np.int32)
-    case = make_replay_case(batch, 16, device, seed=80 + batch, value_heads=value_heads, value_dim=value_dim,
-                            valid=valid, flush=valid == 16, reference_dist=True)
+    batch, value_heads, value_dim, *rest = OTHER_SHAPES[case_id]
+    ring = rest[0] if rest else 16
+    act = rest[1] if len(rest) > 1 else torch.bfloat16
+    plan = gdnr_lib.decode_plan(batch, H, value_heads, value_dim, ring, act=act)
+    assert plan is not None
+    valid = np.where(np.arange(batch) % 2 == 0, ring, 1 + (7 * np.arange(batch)) % (ring - 1)).astype(np.int32)
+    case = make_replay_case(batch, ring, device, seed=80 + batch + ring, value_heads=value_heads, value_dim=value_dim,
+                            dtype=act, valid=valid, flush=valid == ring, reference_dist=True)
     out = run_replay(case, block_v=min(128, value_dim))
     ref, ref_codes, ref_scale = oracle_replay(case, np.float32)
-    fl = valid == 16
+    fl = valid == ring
     codes = codes_np(case["ckpt"].payload)
     err, flips = rel_l2(np32(out), ref), float(np.mean(codes[fl] != ref_codes[fl]))
     print(f"{case_id}: output {err:.3e}, code flips {flips:.2e}")
