@@ -60,7 +60,7 @@ def _hand_built_checkpoint(batch: int, seed: int):
 
 @pytest.mark.parametrize("ring_len,block_v,act", [
     (4, 32, torch.bfloat16), (16, 128, torch.bfloat16), (16, 64, torch.float16), (8, 128, torch.float32),
-    (64, 64, torch.bfloat16), (48, 64, torch.float16)])
+    (64, 64, torch.bfloat16), (48, 64, torch.float16), (64, 64, torch.float32)])
 def test_flush_requantiser_bit_exact(device, ring_len, block_v, act):
     batch = 3
     codes0, scale0, nan_blocks = _hand_built_checkpoint(batch, seed=ring_len + block_v)
