@@ -168,6 +168,14 @@ __device__ __forceinline__ uint32_t ld32(const uint8_t* p) { return *(const uint
 __device__ __forceinline__ uint8_t* sbase(const uint8_t* p, int seq, uint32_t stride) {
   return (uint8_t*)p + (uint64_t)(uint32_t)seq * stride;
 }
+// x + y for two 32-bit products, kept as two multiplies and an add: the fused
+// form (v_mad_u64_u32, whose unused upper addend half the allocator may give
+// a register an outstanding load is filling) makes the wave wait for every
+// load issued before it
+__device__ __forceinline__ uint32_t off_sum(uint32_t x, uint32_t y) {
+  asm volatile("" : "+v"(x), "+v"(y));
+  return x + y;
+}
 // Direct global -> LDS copy of 16 bytes per lane (global_load_lds_dwordx4):
 // lane l's 16 bytes land at LDS address lds_addr + 16 l (lds_addr wave-uniform,
 // through M0, which is restored). Written as inline assembly so that the
@@ -732,13 +740,14 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
     } else {
       qbits = ld32(a.q + (b * a.q_b + h * a.q_h) + 4 * lane);
     }
-    const uint32_t g_raw = *(const uint16_t*)(sbase(a.g, bs, a.g_b) + ((uint32_t)tg * a.g_t + hvr * a.g_h));
-    const uint32_t be_raw = *(const uint16_t*)(sbase(a.beta, bs, a.be_b) + ((uint32_t)tg * a.be_t + hvr * a.be_h));
+    const uint32_t g_raw = *(const uint16_t*)(sbase(a.g, bs, a.g_b) + off_sum((uint32_t)tg * a.g_t, hvr * a.g_h));
+    const uint32_t be_raw =
+        *(const uint16_t*)(sbase(a.beta, bs, a.be_b) + off_sum((uint32_t)tg * a.be_t, hvr * a.be_h));
     uint32_t ab0 = 0, ab1 = 0;
     float alog = 0.f, dtb = 0.f;
     if constexpr (FUSED) {
-      ab0 = gate_bits<GATE_F32>(a.a + (b * a.a_b + hvr * a.a_h));
-      ab1 = gate_bits<GATE_F32>(a.bgate + (b * a.bg_b + hvr * a.bg_h));
+      ab0 = gate_bits<GATE_F32>(a.a + off_sum(b * a.a_b, hvr * a.a_h));
+      ab1 = gate_bits<GATE_F32>(a.bgate + off_sum(b * a.bg_b, hvr * a.bg_h));
       alog = *(const float*)(a.a_log + hvr * a.al_s);
       dtb = *(const float*)(a.dt_bias + hvr * a.db_s);
     }
@@ -842,6 +851,13 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
       xa[m] = x;
       *(u32x4_t*)(ul + kLX + l16 * kXStride + off) = x;
     }
+    // (a replay's row waves take the X rows as their product operands: they
+    // start on them now, not at the flag that publishes the weights)
+    if (!do_flush) {
+      GDNR_WAIT_LGKM0();
+      if (lane == 0)
+        __hip_atomic_store((int*)(ul + kLFlag) + kFlagXRows, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
     // ---- Gram matrix G = X X^T (rows t < n; the query row n gives k_t . q)
     f32x4_t gacc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -924,57 +940,13 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
         acc = fmaf(gcol[t], sv, acc);
       }
       const float c = on ? s_mine * suf_ex : 0.f;
+      // the weights alpha of the X rows: T_0 = sum_t alpha_t X_t (+ lam q for a
+      // full ring) = lam (q - sum_t s_t k_t), the reference's transformed
+      // query; the row waves weight their products S_0 X_t^T with them
       const float al = on ? -lam * s_mine : (l16 == n ? lam : 0.f);
-      if (pub) ((float*)(hl + kHCoef))[l16] = c;
-      // T_0 = sum_t alpha_t X_t (+ lam q for a full ring) = lam (q - sum_t s_t k_t),
-      // the reference's transformed query, per head; lane c2 holds columns
-      // 2 c2, 2 c2 + 1 (the X rows are read once for the heads)
-      float2 xv[NT];
-#pragma unroll
-      for (int t = 0; t < NT; ++t) xv[t] = Act::from_pair(*(const uint32_t*)(ul + kLX + t * kXStride + 4 * lane));
-      const float2 qv = Act::from_pair(*(const uint32_t*)(ul + kLQK + 4 * lane));
-#pragma unroll
-      for (int j = 0; j < kMaxDecodeHeads; ++j) {
-        if (j >= gw) break;
-        float tx = 0.f, ty = 0.f;
-#pragma unroll
-        for (int t = 0; t < NT; ++t) {
-          const float at = rdl(al, 16 * j + t);
-          tx = fmaf(at, xv[t].x, tx);
-          ty = fmaf(at, xv[t].y, ty);
-        }
-        if (full) {
-          const float lj = rdl(lam, 16 * j);
-          tx = fmaf(lj, qv.x, tx);
-          ty = fmaf(lj, qv.y, ty);
-        }
-        // the MFMA operand: T_0 = hi + mid + lo, three 16-bit rows (the f32
-        // value to its last bits); f16 rows are scaled by a power of two
-        // first so that the smaller parts keep their precision
-        float t0s = 1.f;
-        if constexpr (!kBF16) {
-          const float mx =
-              __uint_as_float(wave_max_u32(max(__float_as_uint(fabsf(tx)), __float_as_uint(fabsf(ty)))));
-          if (mx > 0.f && mx < __builtin_inff()) {
-            int ex;
-            (void)frexpf(mx, &ex);
-            ex = uni(ex);
-            tx = ldexpf(tx, -ex);
-            ty = ldexpf(ty, -ex);
-            t0s = ldexpf(1.f, ex);
-          }
-        }
-        const uint32_t hw = act_bits(tx) | (act_bits(ty) << 16);
-        const float2 hv2 = Act::from_pair(hw);
-        const float rx = tx - hv2.x, ry = ty - hv2.y;
-        const uint32_t mw = act_bits(rx) | (act_bits(ry) << 16);
-        const float2 mv2 = Act::from_pair(mw);
-        const uint32_t lw = act_bits(rx - mv2.x) | (act_bits(ry - mv2.y) << 16);
-        uint8_t* hj = ul + kLHeads + j * kHeadLds;
-        *(uint32_t*)(hj + kHT0 + 4 * lane) = hw;
-        *(uint32_t*)(hj + kHT0 + 256 + 4 * lane) = mw;
-        *(uint32_t*)(hj + kHT0 + 512 + 4 * lane) = lw;
-        if (lane == 0) ((float*)(hj + kHLam))[1] = t0s;
+      if (pub) {
+        ((float*)(hl + kHCoef))[l16] = c;
+        ((float*)(hl + kHT0))[l16] = al;
       }
     } else {
       // flush factors (kernel:177-242 in matrix form):
@@ -1421,11 +1393,18 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
   // not a workgroup barrier: the waves of a flushing unit need not wait for
   // the other units' row waves to get their loads issued)
   // (a wait that gives up: the step's output is meaningless, and a flush
-  // stores no codes or scales.) A ring of NCH > 1 chunks, whose chain takes
-  // longer, first stages its v rows (and a replay converts its codes): the
-  // wait comes in each branch.
+  // stores no codes or scales.) A replay of a one-chunk ring in a workgroup
+  // of fewer than 4 units, or of 64-row waves, waits for it after its
+  // products (which take the X rows only): there the chain's time to the
+  // flag is what the step waits for. With 4 units of 128-row waves the
+  // flag comes well before the codes (the stream is the step), and it is
+  // taken here. A ring of NCH > 1 chunks, whose chain takes longer, first
+  // stages its v rows (and a replay converts its codes): the wait comes in
+  // each branch.
+  const bool flag_first = !kEarly && U == 4;
   bool ready_ok = true;
-  if constexpr (!kEarly) ready_ok = wait_flag((int*)(ul + kLFlag) + kFlagReady, A.status, A.wait_polls);
+  if constexpr (!kEarly)
+    if (do_flush || flag_first) ready_ok = wait_flag((int*)(ul + kLFlag) + kFlagReady, A.status, A.wait_polls);
 
   // ring append of the new token's v rows (full contract; this wave's rows,
   // which no other wave reads): the lanes that loaded token pos. (The flush
@@ -1468,9 +1447,13 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
 
   if (!do_flush) {
     // ---- replay: o = (scale S_0 T_0 + sum_t c_t v_t) K^-1/2 ---------------------------
-    // T_0 enters as the A operand rows 0 (hi), 1 (mid) and 2 (lo), the other
-    // rows zero: lanes q4 == 0 get (S_0 T_0)[row] as the sum of their first
-    // three outputs
+    // One-chunk ring: T_0 = sum_t alpha_t X_t (+ lam q for a full ring), so
+    // S_0 T_0 = sum_t alpha_t S_0 X_t: the X rows are the A operand (lane
+    // (row, q4) gets S_0 X_t for t = 4 q4 + e) and each lane weights its four
+    // outputs by alpha; the products need only the X rows, the weights come
+    // with the chain's flag. A ring of NCH > 1 chunks (64 X rows): T_0 enters
+    // as the A operand rows 0 (hi), 1 (mid) and 2 (lo), the other rows zero:
+    // lanes q4 == 0 get (S_0 T_0)[row] as the sum of their first three outputs
     u32x4_t cb[kEarly ? TPW : 1][4];  // (kEarly) the codes as B operands
     uint32_t vwd[NCH][2][4];          // (kEarly) the v words of tiles (2 h, 2 h + 1), token 16 c + 4 q4 + e
     if constexpr (kEarly) {
@@ -1537,28 +1520,69 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
         for (int h = 0; h < 2; ++h)
 #pragma unroll
           for (int e = 0; e < 4; ++e) asm volatile("" : "+v"(vwd[c][h][e]));
-      (void)wait_flag((int*)(ul + kLFlag) + kFlagReady, A.status, A.wait_polls);
+      if constexpr (NCH > 1) (void)wait_flag((int*)(ul + kLFlag) + kFlagReady, A.status, A.wait_polls);
     }
-    const uint8_t* arow = hl + kHT0 + 256 * (l16 < 3 ? l16 : 0) + 64 * q4;
-    const float4 cc = *(const float4*)(hl + kHCoef + 16 * q4);
-    const float t0s = ((const float*)(hl + kHLam))[1];
     // (the codes taken afresh: no conversion here is shared with the flush
     // branch, so none is hoisted above the branch)
 #pragma unroll
     for (int i = 0; i < TPW; ++i) asm volatile("" : "+v"(cw[i][0]), "+v"(cw[i][1]));
     // the products tile by tile as the codes land, then the v terms
     float pt[TPW];
+    if constexpr (NCH == 1) {
+      const bool full = n >= NT;  // (the query not among the X rows)
+      if (!flag_first) (void)wait_flag((int*)(ul + kLFlag) + kFlagXRows, A.status, A.wait_polls);
+      u32x4_t xa[4];
 #pragma unroll
-    for (int i = 0; i < TPW; ++i) {
-      f32x4_t c = {0.f, 0.f, 0.f, 0.f};
+      for (int m = 0; m < 4; ++m) xa[m] = *(const u32x4_t*)(ul + kLX + l16 * kXStride + 64 * q4 + 16 * m);
+      f32x4_t pc[TPW];
+      float pq[TPW];  // (a full ring) S_0 q at lanes q4 == 0: every A row the query
+      // (the full-ring case as a loop of its own: a branch per MFMA would keep
+      // the tiles' MFMA chains from interleaving)
+      auto products = [&](auto with_q) {
 #pragma unroll
-      for (int m = 0; m < 4; ++m) {
-        const u32x4_t x = *(const u32x4_t*)(arow + 16 * m);
-        if constexpr (!kEarly) c = mfma16(l16 < 3 ? x : u32x4_t{0u, 0u, 0u, 0u}, codes8(cw[i], m), c);
-        else c = mfma16(l16 < 3 ? x : u32x4_t{0u, 0u, 0u, 0u}, cb[i][m], c);
+        for (int i = 0; i < TPW; ++i) {
+          f32x4_t c = {0.f, 0.f, 0.f, 0.f}, cq = c;
+#pragma unroll
+          for (int m = 0; m < 4; ++m) {
+            u32x4_t bv;
+            if constexpr (kEarly) bv = cb[i][m];
+            else bv = codes8(cw[i], m);
+            c = mfma16(xa[m], bv, c);
+            if constexpr (decltype(with_q)::value) cq = mfma16(*(const u32x4_t*)(ul + kLQK + 64 * q4 + 16 * m), bv, cq);
+          }
+          pc[i] = c;
+          pq[i] = cq[0];
+        }
+      };
+      if (full) products(std::true_type{});
+      else products(std::false_type{});
+      if (!flag_first) (void)wait_flag((int*)(ul + kLFlag) + kFlagReady, A.status, A.wait_polls);
+      const float4 al = *(const float4*)(hl + kHT0 + 16 * q4);
+      const float lq = (full && q4 == 0) ? ((const float*)(hl + kHLam))[0] : 0.f;
+#pragma unroll
+      for (int i = 0; i < TPW; ++i) {
+        float x = al.x * pc[i][0];
+        x = fmaf(al.y, pc[i][1], x);
+        x = fmaf(al.z, pc[i][2], x);
+        x = fmaf(al.w, pc[i][3], x);
+        x = fmaf(lq, pq[i], x);
+        pt[i] = x * sct[i >> 1];
       }
-      pt[i] = (c[0] + (c[1] + c[2])) * (sct[i >> 1] * t0s);
+    } else {
+      const uint8_t* arow = hl + kHT0 + 256 * (l16 < 3 ? l16 : 0) + 64 * q4;
+      const float t0s = ((const float*)(hl + kHLam))[1];
+#pragma unroll
+      for (int i = 0; i < TPW; ++i) {
+        f32x4_t c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          const u32x4_t x = *(const u32x4_t*)(arow + 16 * m);
+          c = mfma16(l16 < 3 ? x : u32x4_t{0u, 0u, 0u, 0u}, cb[i][m], c);
+        }
+        pt[i] = (c[0] + (c[1] + c[2])) * (sct[i >> 1] * t0s);
+      }
     }
+    const float4 cc = *(const float4*)(hl + kHCoef + 16 * q4);
     float part_[TPW];
     if constexpr (!kEarly) {
       stage_v();
