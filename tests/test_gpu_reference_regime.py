@@ -111,13 +111,20 @@ def test_validate_once_protocol(device, cache_len):
     assert state_err <= VALIDATE_STATE_TOL, state_err
 
 
-def test_replay_every_fill(device):
-    """Gate 3 at every ring fill 0..16 (one sequence each), L = 16."""
-    valid = list(range(17))
-    case = make_replay_case(17, 16, device, seed=31, valid=valid, reference_dist=True)
+@pytest.mark.parametrize("batch", [17, 64])
+def test_replay_every_fill(device, batch):
+    """Gate 3 at every ring fill 0..16, L = 16, no flush (a full ring
+    replays, its query as an operand block of its own). 17 sequences, one per
+    fill (one-unit workgroups, which take their products before the chain's
+    flag), and 64 at fills b mod 17 (the headline's 4-unit workgroups, which
+    take the flag first)."""
+    valid = [b % 17 for b in range(batch)]
+    plan = gdnr_lib.decode_plan(batch, H, 32, 128, 16)
+    assert plan is not None and plan["units"] == (1 if batch == 17 else 4), plan
+    case = make_replay_case(batch, 16, device, seed=31, valid=valid, reference_dist=True)
     out = run_replay(case)
     ref, _, _ = oracle_replay(case)
-    errs = [rel_l2(np32(out)[i], ref[i]) for i in range(17) if valid[i] > 0]
+    errs = [rel_l2(np32(out)[i], ref[i]) for i in range(batch) if valid[i] > 0]
     lam = np.exp(np32(case["g"]).astype(np.float64).cumsum(axis=1)).mean(axis=(0, 2))
     print(f"replay per fill: max {max(errs):.3e}; mean lam at fills 1/4/8/16: {lam[0]:.3f} {lam[3]:.3f} {lam[7]:.3f} "
           f"{lam[15]:.3f}")
