@@ -56,7 +56,8 @@ for _p in (REPO, PKG):
 
 METRIC = "µs per GDN-layer decode step (B=64, L=16) + achieved HBM GB/s % of peak"
 HBM_PEAK_GBS = 8000.0
-KERNEL_NAME = "decode_kernel<8, 1, true, {gate_f32}, false>"  # <tiles per row wave, row waves per head, fused, gate_f32, slots>
+# <tiles per row wave, row waves per head, ring chunks, fused, gate_f32, slots>
+KERNEL_NAME = "decode_kernel<8, 1, 1, true, {gate_f32}, false>"
 CPU_SAMPLE_SECONDS = 10.0
 EXTRAS = ("core", "config1", "split", "config3", "floor")
 CPU_MAX_CYCLES = 8
