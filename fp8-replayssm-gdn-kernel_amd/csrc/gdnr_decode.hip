@@ -266,7 +266,8 @@ constexpr int kFlagHelped = 8;                 // + w: vblocks of row wave w reb
 constexpr int kHCoef = 0;                      // f32 [16]: c_t (replay)
 constexpr int kHLam = kHCoef + 64;             // f32 [4]: lam, the scale of the T_0 rows
 constexpr int kHFac = kHLam + 16;              // float4 [16]: (pre, post, dq, 0) (flush)
-constexpr int kHT0 = kHFac + 256;              // act [3][128]: T_0 as hi, mid and lo rows (replay)
+constexpr int kHT0 = kHFac + 256;              // (replay) f32 [16]: the X rows' weights alpha (one chunk);
+                                               // act [3][128]: T_0 as hi, mid and lo rows (NCH > 1 chunks)
 constexpr int kHM = kHT0;                      // f32 [16][16]: M (chain scratch; flush, so T_0's bytes;
                                                // then the helpers' o partials, [kPartials][64] float2)
 constexpr int kHR = kHM + 1024;                // f32 [16][16]: R = (I + M)^-1 (flush)

@@ -116,8 +116,9 @@ def test_replay_matches_oracle(device, block_v):
 def test_replay_block_v_and_split_identical(device):
     """The tilings (one decode kernel) give bit-identical outputs, and so do
     the two precompute variants of the two-launch split; the split (T_0 in
-    f32, then S_0 T_0) and the one-launch decode (T_0 as three 16-bit MFMA
-    rows) sum in different orders and differ by at most one bf16 ulp."""
+    f32, then S_0 T_0) and the one-launch decode (S_0 X_t for the 16 X rows,
+    weighted by the chain's alpha) sum in different orders and differ by at
+    most one bf16 ulp."""
     case = make_replay_case(4, 8, device, seed=4)
     outs = [run_replay(case, block_v=bv) for bv in (32, 64, 128)]
     for o in outs[1:]:
