@@ -472,7 +472,8 @@ void fill_index(const gdnr_tensor* t, const T** p, int64_t* s) {
 
 // The decode kernel (gdnr_decode.hip) takes 16-bit activations, rings of up
 // to kStepRing tokens and V = 64, 128 or 256 (one wave of 64 or 128 rows per
-// value head, two of 128 rows for V = 256); gw value heads per workgroup
+// value head, four of 32 rows for V = 128 at small batches, two of 128 rows
+// for V = 256); gw value heads per workgroup
 // beside its chain wave. Rings of up to kDecodeChunks kStepRing tokens run
 // as chunks of kStepRing on V = 64 or 128 (one value head per unit, waves of
 // 64 rows). sw carries V / 64 to the launcher.
@@ -499,11 +500,13 @@ void fit_decode(gdnr::ReplayArgs* a) {
   a->nwh = a->V == 256 ? 2 : 1;  // row waves per value head
   a->gw = a->G % 2 == 0 ? 2 : 1;  // value heads per unit (at most 2; they share the unit's chain wave)
   // small batches: one value head per unit (twice the units), and for V = 128
-  // two row waves of 64 rows per head while the units do not outnumber the
+  // four row waves of 32 rows per head while the units do not outnumber the
   // compute units: the launch spreads over the whole chip, and every wave's
-  // share of the stream (and of a flush) is short
+  // share of the stream and of a flush (one vblock) is short. B=8, L=4:
+  // 5.18 us per step against 5.72 with two waves of 64 rows; L=16 4.56
+  // against 4.76; B=16, L=16 5.34 against 5.52.
   if (a->gw == 2 && (int64_t)a->B * a->H * (a->G / 2) < cus) a->gw = 1;
-  if (a->V == 128 && (int64_t)a->B * a->H * (a->G / a->gw) <= cus) a->nwh = 2;
+  if (a->V == 128 && (int64_t)a->B * a->H * (a->G / a->gw) <= cus) a->nwh = 4;
   a->sw = a->V / 64;
   // units per workgroup: as many as fit one CU (12 waves) while the grid
   // still covers every CU; the kernel takes a workgroup's units as SP

@@ -370,9 +370,9 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
   constexpr int kUnitBase = LY::kUnitBase;
   // (row waves) stage their v rows, convert their codes and read back their
   // v words before the chain's flag, rather than after it: a ring of chunks,
-  // and the small-batch shapes (waves of 64 rows), whose launches wait on
-  // their chain; the headline shape (waves of 128 rows) waits on its stream
-  constexpr bool kEarly = NCH > 1 || TPW == 4;
+  // and the small-batch shapes (waves of 32 or 64 rows), whose launches wait
+  // on their chain; the headline shape (waves of 128 rows) waits on its stream
+  constexpr bool kEarly = NCH > 1 || TPW <= 4;
   constexpr int RPW = 16 * TPW;           // V-rows per row wave
   constexpr int VB = TPW / 2;             // vblocks (32 rows) per row wave
   constexpr int VSTRIDE = RPW * ES + 16;  // LDS bytes per token of a row wave's v rows
@@ -1395,7 +1395,7 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
   // the other units' row waves to get their loads issued)
   // (a wait that gives up: the step's output is meaningless, and a flush
   // stores no codes or scales.) A replay of a one-chunk ring in a workgroup
-  // of fewer than 4 units, or of 64-row waves, waits for it after its
+  // of fewer than 4 units, or of 32- or 64-row waves, waits for it after its
   // products (which take the X rows only): there the chain's time to the
   // flag is what the step waits for. With 4 units of 128-row waves the
   // flag comes well before the codes (the stream is the step), and it is
@@ -1440,10 +1440,21 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
   uint8_t* out_rows = A.out + (b * A.o_b + hv * A.o_h + R0 * ES);
   // o of tiles 4 g .. 4 g + 3 from per-tile partials: lane (l16, q4) stores
   // the row of tile 4 g + q4
-  auto store_out = [&](int g, float p0, float p1, float p2, float p3) {
+  auto store_out = [&](int g, float p0, float p1, float p2, float p3, bool keep = true) {
     float o = rows_reduce_scatter(p0, p1, p2, p3);
     asm volatile("" : "+v"(o));  // (no tail shared between the branches)
-    Act::st(out_rows, 64 * g + 32 * (q4 >> 1) + 2 * l16 + (q4 & 1), o * A.out_scale);
+    if (keep) Act::st(out_rows, 64 * g + 32 * (q4 >> 1) + 2 * l16 + (q4 & 1), o * A.out_scale);
+  };
+  // o of every tile from its partials; a wave of 32 rows (2 tiles) stores
+  // from lanes q4 < 2, whose sums take tiles 0 and 1 only (the same sums as
+  // those rows get in a wider wave)
+  auto store_parts = [&](const float* pp) {
+    if constexpr (TPW >= 4) {
+#pragma unroll
+      for (int g = 0; g < TPW / 4; ++g) store_out(g, pp[4 * g], pp[4 * g + 1], pp[4 * g + 2], pp[4 * g + 3]);
+    } else {
+      store_out(0, pp[0], pp[1], 0.f, 0.f, q4 < 2);
+    }
   };
 
   if (!do_flush) {
@@ -1456,7 +1467,8 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
     // as the A operand rows 0 (hi), 1 (mid) and 2 (lo), the other rows zero:
     // lanes q4 == 0 get (S_0 T_0)[row] as the sum of their first three outputs
     u32x4_t cb[kEarly ? TPW : 1][4];  // (kEarly) the codes as B operands
-    uint32_t vwd[NCH][2][4];          // (kEarly) the v words of tiles (2 h, 2 h + 1), token 16 c + 4 q4 + e
+    constexpr int kVH = TPW >= 4 ? 2 : 1;  // (waves of 32 rows: tiles 0 and 1 only)
+    uint32_t vwd[NCH][kVH][4];        // (kEarly) the v words of tiles (2 h, 2 h + 1), token 16 c + 4 q4 + e
     if constexpr (kEarly) {
       if constexpr (NCH > 1) {
       // the chain's Gram groups c >= kChainGroups, round robin over the row
@@ -1511,14 +1523,14 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
 #pragma unroll
       for (int c = 0; c < NCH; ++c)
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
+        for (int h = 0; h < kVH; ++h)
 #pragma unroll
           for (int e = 0; e < 4; ++e)
             vwd[c][h][e] = NT * c < n ? *(const uint32_t*)(vl + (NT * c + 4 * q4 + e) * VSTRIDE + (32 * h + 2 * l16) * ES) : 0u;
 #pragma unroll
       for (int c = 0; c < NCH; ++c)
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
+        for (int h = 0; h < kVH; ++h)
 #pragma unroll
           for (int e = 0; e < 4; ++e) asm volatile("" : "+v"(vwd[c][h][e]));
       if constexpr (NCH > 1) (void)wait_flag((int*)(ul + kLFlag) + kFlagReady, A.status, A.wait_polls);
@@ -1620,8 +1632,7 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
         }
       }
     }
-#pragma unroll
-    for (int g = 0; g < TPW / 4; ++g) store_out(g, part_[4 * g], part_[4 * g + 1], part_[4 * g + 2], part_[4 * g + 3]);
+    store_parts(part_);
     return;
   }
 
@@ -1681,9 +1692,7 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
       for (int k = 0; k < TPW; ++k) opart_all[k] = k == 2 * p ? o2.x : (k == 2 * p + 1 ? o2.y : opart_all[k]);
     }
   }
-#pragma unroll
-  for (int g = 0; g < TPW / 4; ++g)
-    store_out(g, opart_all[4 * g], opart_all[4 * g + 1], opart_all[4 * g + 2], opart_all[4 * g + 3]);
+  store_parts(opart_all);
   if (ready_ok && lane < own) *(uint16_t*)(scale_hv + (vb0 + lane) * A.sc_v) = (uint16_t)new_scale;
   // (with no code stores the loop's count-based DMA waits may have
   // under-counted: drain the last prefetch before the wave ends)
@@ -1735,12 +1744,12 @@ int GDNR_SUFFIX(launch_decode)(const StepArgs& a, bool fused, bool gate_f32, voi
   hipStream_t s = (hipStream_t)stream;
   int rc;
   // V = 64 a.sw: one wave of 64 rows per value head; 128: one of 128 rows,
-  // or two of 64 (small batches); 256: two of 128
+  // or four of 32 (small batches); 256: two of 128
   // (a ring longer than one chunk: waves of 64 rows, one per 64 of V)
   if (a.L > kStepRing) rc = a.sw == 1 ? launch_shape<4, 1, kDecodeChunks>(a, fused, gate_f32, s)
                                       : launch_shape<4, 2, kDecodeChunks>(a, fused, gate_f32, s);
   else if (a.sw == 1) rc = launch_shape<4, 1>(a, fused, gate_f32, s);
-  else if (a.sw == 2 && a.nwh == 2) rc = launch_shape<4, 2>(a, fused, gate_f32, s);
+  else if (a.sw == 2 && a.nwh == 4) rc = launch_shape<2, 4>(a, fused, gate_f32, s);
   else if (a.sw == 2) rc = launch_shape<8, 1>(a, fused, gate_f32, s);
   else rc = launch_shape<8, 2>(a, fused, gate_f32, s);
   if (rc) return rc;

@@ -182,7 +182,8 @@ HEADLINE_CASES = {
     "V256_G1_B64_alternate": (64, 16, 16, 256, "alternate", (128, 2, 1, 4)),
     "V256_G2_B64_alternate": (64, 16, 32, 256, "alternate", (128, 2, 2, 2)),
     "V64_G2_B64_alternate": (64, 16, 32, 64, "alternate", (64, 1, 2, 4)),
-    "V128_G1_B16_alternate": (16, 16, 16, 128, "alternate", (64, 2, 1, 1)),
+    "V128_G1_B16_alternate": (16, 16, 16, 128, "alternate", (32, 4, 1, 1)),
+    "B8_all_flush": (8, 16, 32, 128, "all", (32, 4, 1, 1)),
     "V128_G1_B64_alternate": (64, 16, 16, 128, "alternate", (128, 1, 1, 4)),
     # rings of several 16-token chunks (one value head per unit, waves of 64 rows)
     "L64_B8_all_flush": (8, 16, 32, 128, "all", (64, 2, 1, 1), 64),
