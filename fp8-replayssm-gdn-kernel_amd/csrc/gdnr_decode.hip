@@ -308,10 +308,11 @@ static_assert(Lay<1>::kUnitBase == kUnitBase && Lay<1>::kHR == kHR && Lay<1>::kH
 // and two buffers of one vblock's codes for the flush (4 blocks of 64 x 16
 // bytes): the row wave's prefetch, and a helper's (a ring of nch > 1 chunks
 // takes no helpers: the prefetch buffer only, so that two workgroups of
-// its largest units share a compute unit)
+// its largest units share a compute unit; a wave of one vblock, 32 rows,
+// needs neither)
 constexpr int kVblockBytes = 4 * 64 * 16;
 __host__ __device__ constexpr int row_wave_lds(int nch, int vb) {
-  return NT * nch * (64 * vb + 16) + (nch == 1 ? 2 : 1) * kVblockBytes;
+  return NT * nch * (64 * vb + 16) + (vb > 1 ? (nch == 1 ? 2 : 1) : 0) * kVblockBytes;
 }
 // Vblocks of each row wave of a flushing unit that helpers rebuild (the
 // last ones), given nhelp helper waves: the smallest longest chain
@@ -1745,9 +1746,14 @@ int GDNR_SUFFIX(launch_decode)(const StepArgs& a, bool fused, bool gate_f32, voi
   int rc;
   // V = 64 a.sw: one wave of 64 rows per value head; 128: one of 128 rows,
   // or four of 32 (small batches); 256: two of 128
-  // (a ring longer than one chunk: waves of 64 rows, one per 64 of V)
-  if (a.L > kStepRing) rc = a.sw == 1 ? launch_shape<4, 1, kDecodeChunks>(a, fused, gate_f32, s)
-                                      : launch_shape<4, 2, kDecodeChunks>(a, fused, gate_f32, s);
+  // (a ring longer than one chunk: waves of 32 rows, one per 32 of V, while
+  // a workgroup has a compute unit to itself; else of 64 rows)
+  if (a.L > kStepRing && a.V / a.nwh == 32)
+    rc = a.sw == 1 ? launch_shape<2, 2, kDecodeChunks>(a, fused, gate_f32, s)
+                   : launch_shape<2, 4, kDecodeChunks>(a, fused, gate_f32, s);
+  else if (a.L > kStepRing)
+    rc = a.sw == 1 ? launch_shape<4, 1, kDecodeChunks>(a, fused, gate_f32, s)
+                   : launch_shape<4, 2, kDecodeChunks>(a, fused, gate_f32, s);
   else if (a.sw == 1) rc = launch_shape<4, 1>(a, fused, gate_f32, s);
   else if (a.sw == 2 && a.nwh == 4) rc = launch_shape<2, 4>(a, fused, gate_f32, s);
   else if (a.sw == 2) rc = launch_shape<8, 1>(a, fused, gate_f32, s);

@@ -185,11 +185,14 @@ HEADLINE_CASES = {
     "V128_G1_B16_alternate": (16, 16, 16, 128, "alternate", (32, 4, 1, 1)),
     "B8_all_flush": (8, 16, 32, 128, "all", (32, 4, 1, 1)),
     "V128_G1_B64_alternate": (64, 16, 16, 128, "alternate", (128, 1, 1, 4)),
-    # rings of several 16-token chunks (one value head per unit, waves of 64 rows)
-    "L64_B8_all_flush": (8, 16, 32, 128, "all", (64, 2, 1, 1), 64),
-    "L64_B8_alternate": (8, 16, 32, 128, "alternate", (64, 2, 1, 1), 64),
-    "L48_V64_B8_alternate": (8, 16, 32, 64, "alternate", (64, 1, 1, 1), 48),
-    "L32_V64_B8_all_flush": (8, 16, 32, 64, "all", (64, 1, 1, 1), 32),
+    # rings of several 16-token chunks (one value head per unit; waves of 32
+    # rows while the workgroups do not outnumber the compute units, else 64)
+    "L64_B8_all_flush": (8, 16, 32, 128, "all", (32, 4, 1, 1), 64),
+    "L64_B8_alternate": (8, 16, 32, 128, "alternate", (32, 4, 1, 1), 64),
+    "L48_V64_B8_alternate": (8, 16, 32, 64, "alternate", (32, 2, 1, 1), 48),
+    "L32_V64_B8_all_flush": (8, 16, 32, 64, "all", (32, 2, 1, 1), 32),
+    "L64_B16_alternate": (16, 16, 32, 128, "alternate", (64, 2, 1, 1), 64),
+    "L32_V64_B16_all_flush": (16, 16, 32, 64, "all", (64, 1, 1, 1), 32),
 }
 
 
