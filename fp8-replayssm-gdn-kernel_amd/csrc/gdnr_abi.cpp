@@ -473,10 +473,10 @@ void fill_index(const gdnr_tensor* t, const T** p, int64_t* s) {
 // The decode kernel (gdnr_decode.hip) takes 16-bit activations, rings of up
 // to kStepRing tokens and V = 64, 128 or 256 (one wave of 64 or 128 rows per
 // value head, four of 32 rows for V = 128 at small batches, two of 128 rows
-// for V = 256); gw value heads per workgroup
-// beside its chain wave. Rings of up to kDecodeChunks kStepRing tokens run
-// as chunks of kStepRing on V = 64 or 128 (one value head per unit, waves of
-// 64 rows). sw carries V / 64 to the launcher.
+// for V = 256); gw value heads per workgroup beside its chain wave. Rings
+// of up to kDecodeChunks kStepRing tokens run as chunks of kStepRing on
+// V = 64 or 128 (one value head per unit, waves of 32 or 64 rows). sw
+// carries V / 64 to the launcher.
 bool decode_eligible(const gdnr::ReplayArgs& a, int act) {
   if (act != GDNR_DTYPE_BF16 && act != GDNR_DTYPE_F16) return false;
   if (a.L <= gdnr::kStepRing) return a.V == 64 || a.V == 128 || a.V == 256;
