@@ -380,7 +380,10 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
   const int lane = threadIdx.x & 63;
   const int q4 = lane >> 4, l16 = lane & 15;
   const int w = uni(threadIdx.x >> 6);
-  const int gw = shape & 0xFF, U = shape >> 8;  // value heads per unit, units per workgroup
+  const int gw = shape & 0xFF, U = (shape >> 8) & 0xFF;  // value heads per unit, units per workgroup
+  // workgroups numbered sequence-fastest (grid x = sequences) or head-fastest
+  const bool seq_major = (shape >> 16) != 0;
+  const int bx = (int)(seq_major ? blockIdx.y : blockIdx.x), by = (int)(seq_major ? blockIdx.x : blockIdx.y);
   const int rpu = gw * NWH;                     // row waves per unit
   const bool chain = w < U;                     // waves [0, U): the chain waves
   // (uniform indices: the divisions are VALU code, readfirstlane keeps the
@@ -391,9 +394,9 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
   // over several workgroups, a workgroup's codes over few rows of memory
   const int HP = U == 4 ? 2 : 1, SP = U == 4 ? 2 : U;
   const int uh = HP == 2 ? (u & 1) : 0, us = HP == 2 ? (u >> 1) : u;
-  const int r = uni((int)blockIdx.x * HP + uh);  // the unit's (key head, value-head group)
+  const int r = uni(bx * HP + uh);  // the unit's (key head, value-head group)
   const int n_grp = uni(G / gw);
-  const int h = uni(r / n_grp), grp = r - h * n_grp, b0 = uni((int)blockIdx.y * SP + us);
+  const int h = uni(r / n_grp), grp = r - h * n_grp, b0 = uni(by * SP + us);
   const int hv0 = h * G + grp * gw;              // first value head of the unit
   uint8_t* const ul = lds + u * unit_lds(NCH, rpu, TPW / 2);  // the unit's LDS block
 
@@ -1709,7 +1712,8 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
 template <int TPW, int NWH, int NCH, bool FUSED, bool GATE_F32, bool SLOTS>
 int launch_variant(const StepArgs& a, hipStream_t s) {
   const int hp = a.units == 4 ? 2 : 1, sp = a.units / hp;  // as in the kernel
-  const dim3 grid((unsigned)(a.H * (a.G / a.gw) / hp), (unsigned)(a.B / sp)),
+  const unsigned gh = (unsigned)(a.H * (a.G / a.gw) / hp), gs = (unsigned)(a.B / sp);
+  const dim3 grid(a.seq_major ? gs : gh, a.seq_major ? gh : gs),
       block((unsigned)(64 * a.units * (1 + a.gw * NWH)));
   auto kernel = decode_kernel<TPW, NWH, NCH, FUSED, GATE_F32, SLOTS>;
   if (a.lds_bytes > 64 * 1024) {
@@ -1718,7 +1722,7 @@ int launch_variant(const StepArgs& a, hipStream_t s) {
     if (e != hipSuccess) return (int)e;
   }
   hipLaunchKernelGGL(kernel, grid, block, a.lds_bytes, s, a.ckpt, a.k, a.ck_b, a.ck_h, a.ck_v, a.k_b, a.k_t, a.k_h,
-                     a.L, a.G, a.gw | (a.units << 8), a);
+                     a.L, a.G, a.gw | (a.units << 8) | (a.seq_major << 16), a);
   return 0;
 }
 

@@ -59,6 +59,7 @@ struct ReplayArgs {
   int32_t sw, rpw, lds_knew, lds_flag, lds_c, lds_g;
   int32_t units;  // decode kernel: (key head, value-head group) units per workgroup
   int32_t nwh;    // decode kernel: row waves per value head
+  int32_t seq_major;  // decode kernel: workgroups numbered sequence-fastest (grid x = sequences)
   // flush (MFMA rebuild), per head: R = (I + M)^-1 [16 x 16] f32, per-token
   // factors (pre, post, dq, -) f32, lam_all f32; K^T operand tiles [K x 16]
   // in the ring dtype; per-head scratch (3 KiB)
@@ -85,7 +86,7 @@ struct StepArgs {
   uint32_t ck_b, ck_h, ck_v, sc_b, sc_h, sc_v, q_b, q_h, k_b, k_t, k_h, v_b, v_t, v_h;
   uint32_t g_b, g_t, g_h, be_b, be_t, be_h, vl_s, fl_s, pos_s, o_b, o_h, mx_b;
   uint32_t a_b, a_h, bg_b, bg_h, al_s, db_s, qo_b, qo_h;
-  int32_t B, H, G, V, L, gw, block_v, n_vt, sw, rpw, units, nwh;
+  int32_t B, H, G, V, L, gw, block_v, n_vt, sw, rpw, units, nwh, seq_major;
   float out_scale;
   int32_t lds_q, lds_knew, lds_k, lds_flag, lds_c, lds_t, lds_g, lds_v, lds_r, lds_fac, lds_kt, lds_lam, lds_u, lds_bytes;
   // slot indirection (fused step only): sequence b's checkpoint, scale and
