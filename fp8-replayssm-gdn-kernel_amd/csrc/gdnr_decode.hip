@@ -243,6 +243,27 @@ __device__ __forceinline__ float rows_reduce_scatter(float p0, float p1, float p
   return __uint_as_float(r2[0]) + __uint_as_float(r2[1]);
 }
 
+// The U~ operand of a flush's K^T U~ MFMA (16x16x32, k-slot 8 q4 + j) from
+// this lane's 16-bit hi and lo words of tokens 4 q4 .. 4 q4 + 3 (h01 = hi
+// of tokens 4 q4 and 4 q4 + 1, ...). One half-wave swap per word pair gives
+// lanes q4 < 2 the hi words of tokens 4 q4 .. +3 and 4 q4 + 8 .. +3, lanes
+// q4 >= 2 the lo words of tokens 4 q4 - 8 .. -5 and 4 q4 .. +3: k-slots
+// 8 q4 .. 8 q4 + 7 hold positions 8 (q4 & 1) .. + 7 of kt_pos's token order.
+__device__ __forceinline__ u32x4_t utilde_operand(uint32_t h01, uint32_t h23, uint32_t l01, uint32_t l23) {
+  const auto s01 = __builtin_amdgcn_permlane32_swap(h01, l01, false, false);
+  const auto s23 = __builtin_amdgcn_permlane32_swap(h23, l23, false, false);
+  return u32x4_t{s01[0], s23[0], s01[1], s23[1]};
+}
+// max(m, |a|, |b|), NaN propagating (one v_maximum3_f32)
+__device__ __forceinline__ float max3_abs(float m, float a, float b) {
+  return __builtin_elementwise_maximum(__builtin_elementwise_maximum(m, __builtin_fabsf(a)), __builtin_fabsf(b));
+}
+// Position of token t in a row of the flush's K^T tiles (bits 2 and 3
+// swapped: positions 0..7 hold tokens 0..3 and 8..11, positions 8..15
+// tokens 4..7 and 12..15), so that lane (nn, q4) reads its 8 operand words
+// as one 16-byte read at position 8 (q4 & 1).
+__device__ __forceinline__ int kt_pos(int t) { return (t & 3) | ((t & 4) << 1) | ((t & 8) >> 1); }
+
 extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
 
 // LDS of a workgroup (bytes). A unit's chain wave writes its blocks before
@@ -450,14 +471,24 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
   // the codes are no longer needed.
   //
   // S_n column group ct of tile ii: lane (nn, q4) gets
-  // S_n[row r(ii, nn)][32 q4 + 4 ct + e], code byte 4 ct + e of its 32. lam
-  // S_0 enters through the MFMA as (ls I) S_0^T with ls = lam * scale split
-  // into hi + lo halves; each hi/lo pair is one 16x16x32 MFMA (k-slots
-  // 8 q4 + j: j < 4 the hi part, j >= 4 the lo part of column 4 q4 + (j & 3)).
+  // S_n[row r(ii, nn)][32 q4 + 4 ct + e], code byte 4 ct + e of its 32. The
+  // update K^T U~ is one 16x16x32 MFMA per group with U~ split into hi + lo
+  // halves (k-slots 8 q4 + j: j < 4 the hi part, j >= 4 the lo part of token
+  // 4 q4 + (j & 3)); lam S_0 is its accumulator input.
   auto flush_vblock = [&](const uint8_t* uu, const uint8_t* hb, const uint8_t* vr, int nf, const u32x4_t (&c)[2][2],
                           float scp, uint8_t* rows, int p, bool st, float* op, auto&& after_pass1) -> float {
     // (lam of the whole ring; of chunk 0 for a ring of NCH > 1 chunks)
     const float lamv = ((const float*)(hb + kHLam))[NCH == 1 ? 0 : 2];
+    // One chunk, bf16 operands: ls = lam scale is folded out of the state.
+    // The MFMA accumulates A = code + K^T (U~ / ls) (the codes enter
+    // unscaled), the amax is ls max|A| (rounding is monotone, so it equals
+    // the max of the rounded products), and the quotient multiplies A by
+    // RN64(ls / s): for a state ls A that is a float this is within 2^-52 of
+    // x / s, the bound quotient_f64 needs. That saves one multiply per
+    // element. Taken while 1 / ls and U~ / ls stay in range.
+    const float ls = lamv * scp;
+    const bool fold = NCH == 1 && kBF16 && uni((int)(ls >= 0x1p-64f && ls <= 0x1p64f)) != 0;
+    const float rls = fold ? __builtin_amdgcn_rcpf(ls) : 1.0f;  // (1 ulp: U~ / ls is an operand, not a result)
     u32x4_t packed[2];
 #pragma unroll
     for (int ii = 0; ii < 2; ++ii) {
@@ -502,13 +533,13 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
       }
       op[ii] = o;
       if constexpr (kBF16) {
-        // hi/lo split: U~ = hi + lo to ~16 bits, both halves bf16 operands
-        const uint32_t h01 = pack_bf16x2(ut[0], ut[1]), h23 = pack_bf16x2(ut[2], ut[3]);
-        const uint32_t l01 =
-            pack_bf16x2(ut[0] - __uint_as_float(h01 << 16), ut[1] - __uint_as_float(h01 & 0xFFFF0000u));
-        const uint32_t l23 =
-            pack_bf16x2(ut[2] - __uint_as_float(h23 << 16), ut[3] - __uint_as_float(h23 & 0xFFFF0000u));
-        packed[ii] = u32x4_t{h01, h23, l01, l23};
+        // hi/lo split: U~ (/ ls when folded) = hi + lo to ~16 bits, both
+        // halves bf16 operands
+        const float u0 = ut[0] * rls, u1 = ut[1] * rls, u2 = ut[2] * rls, u3 = ut[3] * rls;
+        const uint32_t h01 = pack_bf16x2(u0, u1), h23 = pack_bf16x2(u2, u3);
+        const uint32_t l01 = pack_bf16x2(u0 - __uint_as_float(h01 << 16), u1 - __uint_as_float(h01 & 0xFFFF0000u));
+        const uint32_t l23 = pack_bf16x2(u2 - __uint_as_float(h23 << 16), u3 - __uint_as_float(h23 & 0xFFFF0000u));
+        packed[ii] = utilde_operand(h01, h23, l01, l23);
       } else {
         _Float16 hh[4], ll[4];
 #pragma unroll
@@ -519,7 +550,7 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
         auto pk = [](_Float16 x, _Float16 y) {
           return (uint32_t)__builtin_bit_cast(uint16_t, x) | ((uint32_t)__builtin_bit_cast(uint16_t, y) << 16);
         };
-        packed[ii] = u32x4_t{pk(hh[0], hh[1]), pk(hh[2], hh[3]), pk(ll[0], ll[1]), pk(ll[2], ll[3])};
+        packed[ii] = utilde_operand(pk(hh[0], hh[1]), pk(hh[2], hh[3]), pk(ll[0], ll[1]), pk(ll[2], ll[3]));
       }
     }
     // pass 1: S_n of the vblock's 2 x 8 column groups (kept) and the vblock
@@ -530,19 +561,25 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
     f32x4_t sv[2][8];
     float am = 0.f;
     {
-      const float ls = lamv * scp;
+      auto pass1 = [&](auto folded) {
 #pragma unroll
-      for (int ct = 0; ct < 8; ++ct) {
+        for (int ct = 0; ct < 8; ++ct) {
 #pragma unroll
-        for (int ii = 0; ii < 2; ++ii) {
-          const uint32_t cw4 = c[ii][ct >> 2][ct & 3];
-          const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)cw4, false);
-          const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)cw4, true);
-          const f32x4_t s0 = {ls * lo[0], ls * lo[1], ls * hi[0], ls * hi[1]};
-          const uint2 k2 = *(const uint2*)(uu + kLKT + 2 * ((ct * 16 + l16) * 16 + 4 * q4));
-          sv[ii][ct] = mfma16(u32x4_t{k2.x, k2.y, k2.x, k2.y}, packed[ii], s0);
+          for (int ii = 0; ii < 2; ++ii) {
+            const uint32_t cw4 = c[ii][ct >> 2][ct & 3];
+            const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)cw4, false);
+            const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)cw4, true);
+            const f32x4_t s0 = decltype(folded)::value ? f32x4_t{lo[0], lo[1], hi[0], hi[1]}
+                                                       : f32x4_t{ls * lo[0], ls * lo[1], ls * hi[0], ls * hi[1]};
+            const u32x4_t k8 = *(const u32x4_t*)(uu + kLKT + 32 * (ct * 16 + l16) + 16 * (q4 & 1));
+            sv[ii][ct] = mfma16(k8, packed[ii], s0);
+          }
         }
-      }
+      };
+      if (fold)
+        pass1(std::true_type{});
+      else
+        pass1(std::false_type{});
       if constexpr (NCH > 1) {
         // (the codes are not needed past chunk 0)
         after_pass1();
@@ -608,39 +645,42 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
               const float2 hv = Act::from_pair(h2[w2]);
               l2[w2] = act_bits(ut[2 * w2] - hv.x) | (act_bits(ut[2 * w2 + 1] - hv.y) << 16);
             }
-            pk2[ii] = u32x4_t{h2[0], h2[1], l2[0], l2[1]};
+            pk2[ii] = utilde_operand(h2[0], h2[1], l2[0], l2[1]);
           }
 #pragma unroll
           for (int ct = 0; ct < 8; ++ct) {
 #pragma unroll
             for (int ii = 0; ii < 2; ++ii) {
-              const uint2 k2 = *(const uint2*)(uu + kLKT + cc * (8 * 16 * 16 * 2) +
-                                               2 * ((ct * 16 + l16) * 16 + 4 * q4));
+              const u32x4_t k8 = *(const u32x4_t*)(uu + kLKT + cc * (8 * 16 * 16 * 2) + 32 * (ct * 16 + l16) +
+                                                   16 * (q4 & 1));
               const f32x4_t acc = sv[ii][ct] * lc;
-              sv[ii][ct] = mfma16(u32x4_t{k2.x, k2.y, k2.x, k2.y}, pk2[ii], acc);
+              sv[ii][ct] = mfma16(k8, pk2[ii], acc);
             }
           }
         }
       }
+      // (two running maxima, each taking two elements per instruction)
+      float am1 = 0.f;
 #pragma unroll
       for (int ct = 0; ct < 8; ++ct) {
 #pragma unroll
         for (int ii = 0; ii < 2; ++ii) {
           const f32x4_t sg = sv[ii][ct];
-          am = __builtin_elementwise_maximum(am, __builtin_elementwise_maximum(__builtin_fabsf(sg[0]), __builtin_fabsf(sg[1])));
-          am = __builtin_elementwise_maximum(am, __builtin_elementwise_maximum(__builtin_fabsf(sg[2]), __builtin_fabsf(sg[3])));
+          am = max3_abs(am, sg[0], sg[1]);
+          am1 = max3_abs(am1, sg[2], sg[3]);
         }
       }
+      am = __builtin_elementwise_maximum(am, am1);
     }
     if constexpr (NCH == 1) after_pass1();
-    const uint32_t amb = wave_max_u32(__float_as_uint(am));
     // the reference quantiser (ref:36-37,83-99): s = amax / 448 (1 when amax
     // is not > 0); codes = e4m3fn(clamp(x / s, +-448)) with the unrounded s;
-    // the quotient by quotient_f64 when the block is finite
-    const float amax = __uint_as_float(amb);
+    // the quotient by quotient_f64 when the block is finite (x = xs A)
+    const float xs = fold ? ls : 1.0f;
+    const float amax = xs * __uint_as_float(wave_max_u32(__float_as_uint(am)));
     const float s32 = (amax > 0.0f) ? amax / 448.0f : 1.0f;
-    const bool fast = quotient_fast(amb, s32);
-    const double r64 = 1.0 / (double)s32;
+    const bool fast = quotient_fast(__float_as_uint(amax), s32);
+    const double r64 = (double)xs / (double)s32;
     // pass 2: the kept column groups requantised and stored (the division
     // path of non-finite or tiny-scale blocks is a loop of its own)
     auto pass2 = [&](auto quant) {
@@ -668,7 +708,7 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
         float qv[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          qv[e] = v[e] / s32;
+          qv[e] = (xs * v[e]) / s32;
           __builtin_amdgcn_sched_barrier(0);
         }
         const uint32_t wd = f32x4_to_fp8_ref_cold(qv[0], qv[1], qv[2], qv[3]);
@@ -895,10 +935,10 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
     }
     const float dq = on ? (full ? Dq[l16] : Gs[l16 * 16 + (full ? 0 : n)]) : 0.f;
     if (do_flush) {
-      // K^T operand tiles [ct][M][token] (flush): element (t, col) of X with
-      // col = 32 q4 + 8 m + j8 goes to tile ct = 2 m + j8 / 4, row
-      // M = 4 q4 + j8 % 4 (tile ct, row M: column 32 (M >> 2) + 4 ct + (M & 3));
-      // tokens t >= n are zero
+      // K^T operand tiles [ct][M][position] (flush): element (t, col) of X
+      // with col = 32 q4 + 8 m + j8 goes to tile ct = 2 m + j8 / 4, row
+      // M = 4 q4 + j8 % 4 (tile ct, row M: column 32 (M >> 2) + 4 ct + (M & 3)),
+      // position kt_pos(t); tokens t >= n are zero
       uint16_t* kt = (uint16_t*)(ul + kLKT);
 #pragma unroll
       for (int m = 0; m < 4; ++m) {
@@ -906,7 +946,7 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
 #pragma unroll
         for (int j8 = 0; j8 < 8; ++j8) {
           const uint16_t e16 = (uint16_t)((x[j8 >> 1] >> (16 * (j8 & 1))) & 0xFFFFu);
-          kt[((2 * m + (j8 >> 2)) * 16 + 4 * q4 + (j8 & 3)) * 16 + l16] = e16;
+          kt[((2 * m + (j8 >> 2)) * 16 + 4 * q4 + (j8 & 3)) * 16 + kt_pos(l16)] = e16;
         }
       }
     }
@@ -1059,7 +1099,7 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
 #pragma unroll
           for (int j8 = 0; j8 < 8; ++j8) {
             const uint16_t e16 = (uint16_t)((x[j8 >> 1] >> (16 * (j8 & 1))) & 0xFFFFu);
-            kt[((2 * m + (j8 >> 2)) * 16 + 4 * q4 + (j8 & 3)) * 16 + l16] = e16;
+            kt[((2 * m + (j8 >> 2)) * 16 + 4 * q4 + (j8 & 3)) * 16 + kt_pos(l16)] = e16;
           }
         }
       }

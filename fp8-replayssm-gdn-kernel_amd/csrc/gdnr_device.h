@@ -163,7 +163,9 @@ __device__ __forceinline__ uint2 fp8x4_to_f16x4(uint32_t w) {
 }
 // 4 floats -> 4 packed codes, round-to-nearest-even (inputs already clamped).
 __device__ __forceinline__ uint32_t f32x4_to_fp8(float a, float b, float c, float d) {
-  int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  // (the first convert writes bytes 0-1 and keeps the word's other half,
+  // which the second overwrites: a's bits as that half spare a register copy)
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, __float_as_int(a), false);
   w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
   return (uint32_t)w;
 }
