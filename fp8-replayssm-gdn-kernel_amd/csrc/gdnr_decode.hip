@@ -1443,28 +1443,13 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
   // products (which take the X rows only): there the chain's time to the
   // flag is what the step waits for. With 4 units of 128-row waves the
   // flag comes well before the codes (the stream is the step), and it is
-  // taken here. A ring of NCH > 1 chunks, whose chain takes longer, first
-  // stages its v rows (and a replay converts its codes): the wait comes in
-  // each branch.
+  // taken first, as in a flush. A ring of NCH > 1 chunks, whose chain takes
+  // longer, first stages its v rows (and a replay converts its codes). (The
+  // waits sit in each branch, so that the flush's early request of its next
+  // codes is on the flush's path only: a path joining the replay's after it
+  // would make the compiler's waits for the v rows cover it.)
   const bool flag_first = !kEarly && U == 4;
   bool ready_ok = true;
-  if constexpr (!kEarly)
-    if (do_flush || flag_first) ready_ok = wait_flag((int*)(ul + kLFlag) + kFlagReady, A.status, A.wait_polls);
-
-  // ring append of the new token's v rows (full contract; this wave's rows,
-  // which no other wave reads): the lanes that loaded token pos. (The flush
-  // appends from LDS after its loop: no store is outstanding when the loop
-  // starts, so its waits for each vblock's codes never cover a store.)
-  if constexpr (FUSED) {
-    if (pos >= 0 && !do_flush) {
-      uint8_t* vw = sbase(A.v, bs, A.v_b) + ((uint32_t)pos * A.v_t + hv * A.v_h + R0 * ES) + 16 * vpiece;
-#pragma unroll
-      for (int c = 0; c < NCH; ++c)
-#pragma unroll
-        for (int k = 0; k < NVL; ++k)
-          if (NT * c + vtok(k) == pos) *(u32x4_t*)vw = vq[c][k];
-    }
-  }
   // the v rows go to LDS token-major ([16][VS] bytes; the replay once its
   // products are issued, the flush first): lane (nn, q4) then reads the two
   // rows of tiles (2p, 2p + 1) of token 4 q4 + e as one word
@@ -1503,6 +1488,22 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
 
   if (!do_flush) {
     // ---- replay: o = (scale S_0 T_0 + sum_t c_t v_t) K^-1/2 ---------------------------
+    if constexpr (!kEarly)
+      if (flag_first) ready_ok = wait_flag((int*)(ul + kLFlag) + kFlagReady, A.status, A.wait_polls);
+    // ring append of the new token's v rows (full contract; this wave's
+    // rows, which no other wave reads): the lanes that loaded token pos. (The
+    // flush appends from LDS after its loop: no store is outstanding when the
+    // loop starts, so its waits for each vblock's codes never cover a store.)
+    if constexpr (FUSED) {
+      if (pos >= 0) {
+        uint8_t* vw = sbase(A.v, bs, A.v_b) + ((uint32_t)pos * A.v_t + hv * A.v_h + R0 * ES) + 16 * vpiece;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c)
+#pragma unroll
+          for (int k = 0; k < NVL; ++k)
+            if (NT * c + vtok(k) == pos) *(u32x4_t*)vw = vq[c][k];
+      }
+    }
     // One-chunk ring: T_0 = sum_t alpha_t X_t (+ lam q for a full ring), so
     // S_0 T_0 = sum_t alpha_t S_0 X_t: the X rows are the A operand (lane
     // (row, q4) gets S_0 X_t for t = 4 q4 + e) and each lane weights its four
@@ -1681,21 +1682,25 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
   }
 
   // ---- flush: the wave's vblocks in turn (flush_vblock); the last nh of
-  // them rebuilt by helper waves, whose o shares come back through LDS
+  // them rebuilt by helper waves, whose o shares come back through LDS.
+  // The v rows go to LDS first; then vblock 1's codes go to the prefetch
+  // buffer, long before vblock 0 is rebuilt, and only then does the wave
+  // wait for the chain's flag. (Staged after that request, the v rows would
+  // wait for it: the compiler's waits before the LDS writes cover the DMA.)
   stage_v();
-  if constexpr (kEarly) ready_ok = wait_flag((int*)(ul + kLFlag) + kFlagReady, A.status, A.wait_polls);
   int* const flags = (int*)(ul + kLFlag);
   if (lane == 0) __hip_atomic_store(flags + kFlagVStaged + wr, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
   const int own = VB - nh;
+  if (own > 1) dma_vblock(ck_rows, 1, pf);
+  ready_ok = wait_flag((int*)(ul + kLFlag) + kFlagReady, A.status, A.wait_polls);
   u32x4_t cur[2][2] = {{cw[0][0], cw[0][1]}, {cw[1][0], cw[1][1]}};
   // The codes of vblock p + 1 come from the wave's prefetch buffer, which
   // direct DMA fills while vblock p - 1 is finished and p is rebuilt. Each
   // iteration issues its DMA and then exactly 4 stores, so "4 outstanding"
-  // means the DMA of the iteration before has landed (the first iteration's,
-  // issued before the loop, is the only request outstanding). (Issued here,
-  // not with vblock 0: ahead of the v rows it would delay the first vblock.)
-  // (tiles 0 and 1 have landed: stage_v waited for the v rows, read after them)
-  if (own > 1) dma_vblock(ck_rows, 1, pf);
+  // means the DMA of the iteration before has landed (the first iteration's
+  // wait takes everything: vblock 1's DMA, issued after the v rows, is then
+  // the only request outstanding). (Not with vblock 0's rows: ahead of the v
+  // rows it would delay the first vblock.)
   // (a loop, not unrolled: one vblock's registers at a time; the indices
   // that depend on p are formed by selects, not by indexing registers)
   float opart_all[TPW];
