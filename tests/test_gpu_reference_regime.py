@@ -280,21 +280,27 @@ def test_other_decode_shapes(device, case_id):
 LAMBDA_FLIP_TOL = 1e-4
 
 
-@pytest.mark.parametrize("ring_len", [4, 16, 64])
-def test_lambda_path_flush(device, ring_len):
+@pytest.mark.parametrize("ring_len,regime", [(4, "mid"), (16, "mid"), (64, "mid"), (16, "tiny"), (64, "tiny")])
+def test_lambda_path_flush(device, ring_len, regime):
     """beta = 0 on every token and a constant g_h < 0 per (sequence, head), so
-    the flush rebuilds lam S_0 with lam = exp(L g_h) in 0.3 .. 0.9: the decode
-    kernel forms it as (lam scale) x code, the oracle as the fp32 recurrence
-    S <- exp(g) S token by token (ref:155-161), then the reference quantiser.
-    Codes may differ only where the two roundings straddle an e4m3 rounding
-    boundary (< 1e-4 of the codes); scales within one fp16 ulp. B = 64 with
-    alternate sequences flushing (helpers rebuild some vblocks)."""
+    the flush rebuilds lam S_0 with lam = exp(L g_h): in 0.3 .. 0.9 ("mid"),
+    or log-uniform in 1e-28 .. 1e-6 ("tiny": lam scale on both sides of
+    2^-64, where the one-chunk decode rebuild stops folding lam scale into
+    the quotient and forms (lam scale) x code instead). The oracle is the
+    fp32 recurrence S <- exp(g) S token by token (ref:155-161), then the
+    reference quantiser. Codes may differ only where the two roundings
+    straddle an e4m3 rounding boundary (< 1e-4 of the codes); scales within
+    one fp16 ulp. B = 64 with alternate sequences flushing (helpers rebuild
+    some vblocks)."""
     batch = 64
     valid = np.where(np.arange(batch) % 2 == 0, ring_len, 1).astype(np.int32)
     case = make_replay_case(batch, ring_len, device, seed=90 + ring_len, valid=valid, flush=valid == ring_len,
                             reference_dist=True)
     gen = torch.Generator().manual_seed(ring_len)
-    lam = torch.rand(batch, 1, HV, generator=gen) * 0.6 + 0.3
+    if regime == "mid":
+        lam = torch.rand(batch, 1, HV, generator=gen) * 0.6 + 0.3
+    else:
+        lam = 10.0 ** (torch.rand(batch, 1, HV, generator=gen, dtype=torch.float64) * -22.0 - 6.0)
     g = (lam.log() / ring_len).expand(batch, ring_len, HV).to(torch.bfloat16)
     case["g"] = g.contiguous().to(device)
     case["beta"] = torch.zeros_like(case["beta"])
@@ -305,9 +311,12 @@ def test_lambda_path_flush(device, ring_len):
     flips = float(np.mean(codes[fl] != ref_codes[fl]))
     ulps = _fp16_ulps(case["ckpt"].scale.cpu().numpy()[fl], ref_scale[fl])
     realised = np.exp(np32(case["g"]).astype(np.float64).sum(axis=1))[fl]
-    print(f"lam path L={ring_len}: lam {realised.min():.3f}..{realised.max():.3f}, code flips {flips:.2e}, "
+    print(f"lam path L={ring_len} {regime}: lam {realised.min():.3g}..{realised.max():.3g}, code flips {flips:.2e}, "
           f"scale ulps max {ulps.max()} (mean {ulps.mean():.2e})")
-    assert realised.min() > 0.25 and realised.max() < 0.95
+    if regime == "mid":
+        assert realised.min() > 0.25 and realised.max() < 0.95
+    else:
+        assert realised.min() < 1e-25 and realised.max() > 1e-9
     assert flips < LAMBDA_FLIP_TOL, flips
     assert ulps.max() <= 1
     assert rel_l2(np32(out), ref) <= OUT_TOL
