@@ -260,8 +260,8 @@ __device__ __forceinline__ float max3_abs(float m, float a, float b) {
 }
 // Position of token t in a row of the flush's K^T tiles (bits 2 and 3
 // swapped: positions 0..7 hold tokens 0..3 and 8..11, positions 8..15
-// tokens 4..7 and 12..15), so that lane (nn, q4) reads its 8 operand words
-// as one 16-byte read at position 8 (q4 & 1).
+// tokens 4..7 and 12..15), so that lane (nn, q4) reads its 8 16-bit operand
+// values as one 16-byte read at position 8 (q4 & 1).
 __device__ __forceinline__ int kt_pos(int t) { return (t & 3) | ((t & 4) << 1) | ((t & 8) >> 1); }
 
 extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -473,8 +473,8 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void d
   // S_n column group ct of tile ii: lane (nn, q4) gets
   // S_n[row r(ii, nn)][32 q4 + 4 ct + e], code byte 4 ct + e of its 32. The
   // update K^T U~ is one 16x16x32 MFMA per group with U~ split into hi + lo
-  // halves (k-slots 8 q4 + j: j < 4 the hi part, j >= 4 the lo part of token
-  // 4 q4 + (j & 3)); lam S_0 is its accumulator input.
+  // halves (k-slots in utilde_operand's token order); its accumulator input
+  // is lam S_0, or the codes alone when lam scale is folded out (below).
   auto flush_vblock = [&](const uint8_t* uu, const uint8_t* hb, const uint8_t* vr, int nf, const u32x4_t (&c)[2][2],
                           float scp, uint8_t* rows, int p, bool st, float* op, auto&& after_pass1) -> float {
     // (lam of the whole ring; of chunk 0 for a ring of NCH > 1 chunks)
